@@ -1,0 +1,160 @@
+/* C ABI of libssa_hip.so: clustered sparse decode attention on AMD Instinct MI355X (gfx950).
+ *
+ * Every entry point takes device pointers, element strides, sizes and a hipStream_t passed as
+ * void*, enqueues its kernels on that stream and returns a hipError_t value (0 = success). None
+ * of them allocates device memory, synchronizes, or reads device memory on the host, so all of
+ * them can be captured in a hipGraph. Lengths that change from step to step can be given in
+ * device memory (n_dev, the index's end[]), which keeps a captured graph valid across steps.
+ *
+ * dtype tags: 0 = float32, 1 = bfloat16, 2 = float16.
+ *
+ * Layouts follow the reference's engine cache: K, V are [Hk, capacity, d] with a unit last
+ * stride (Hk = batch x KV heads), q is [Hk*G, d], labels are int16 [Hk, capacity] with label C
+ * marking the always-read exact set (token 0 and the recent window), w is fp32 [Hk or Hk*G, C+1].
+ */
+#ifndef SSA_HIP_H
+#define SSA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Text of a hipError_t value returned by the entry points below. */
+const char* ssa_error_string(int err);
+
+/* ---- attention ----------------------------------------------------------------------------- */
+
+typedef struct ssa_attn_args {
+  const void* q; int64_t s_qh; int32_t q_dtype;
+  const void* k; int64_t s_kh; int64_t s_kn;
+  const void* v; int64_t s_vh; int64_t s_vn;
+  int32_t kv_dtype;
+  const int16_t* labels; int64_t s_lh;      /* labelled mode only */
+  const float* w; int64_t s_wr; int32_t w_len; int32_t per_head;
+  const int32_t* n_dev; int32_t n_host;      /* positions [0, n) are attended; n_dev wins if set */
+  float* part_m; float* part_l;              /* [Hk, S, G] split partials (base-2 log domain) */
+  float* part_a;                             /* [Hk, S, G, d] */
+  int32_t* part_cnt;                         /* [Hk, S] rows read per split */
+  int32_t* counter;                          /* [Hk] zero on first use; the kernel leaves it zero */
+  void* out; int64_t s_oh; int32_t out_dtype;/* [Hk*G, d] */
+  int32_t* cnt_out;                          /* optional [Hk]: rows read per KV head */
+  int32_t n_heads; int32_t G; int32_t d; int32_t S; int32_t chunk_align;
+} ssa_attn_args_t;
+
+/* Label-weighted split-K decode attention with the compaction fused in: positions whose label
+ * has positive weight (for any query head of the group when per_head) are read, each with
+ * weight w; the S partials of a head are merged by log-sum-exp in the same launch.
+ * Replaces label_weighted_attention_compact (src/ssa/kernels/labeled_attn.py:248-278), i.e.
+ * compact_positions + _list_kernel + merge_splits (:186, :203, :143), and the masked-scan
+ * label_weighted_attention_triton (:88). Spec: label_weighted_attention (src/ssa/attn/labeled.py:24). */
+int ssa_label_attention(const ssa_attn_args_t* args, void* stream);
+
+/* Exact split-K decode attention over [0, n) (labels and w ignored).
+ * Replaces DenseAttentionGraph.__call__ / _dense_dev_kernel (src/ssa/kernels/graph_kernels.py:28-59,171-189). */
+int ssa_dense_attention(const ssa_attn_args_t* args, void* stream);
+
+/* Log-sum-exp merge of natural-log split partials m, l [Hk, S, G] and a [Hk, S, G, d] into
+ * out [Hk*G, d]. Replaces merge_splits / _merge_kernel (src/ssa/kernels/labeled_attn.py:124-151). */
+int ssa_merge_splits(const float* m, const float* l, const float* a, int64_t s_mh, int64_t s_ms,
+                     int64_t s_ah, int64_t s_as, int64_t s_ag, int n_heads, int S, int G, int d,
+                     void* out, int64_t s_oh, int out_dtype, void* stream);
+
+/* Ascending list of the selected positions {j < n : w[labels[j]] > 0} per KV head: idx
+ * [Hk, >= n] (first cnt[h] valid), cnt [Hk]. block_counts is scratch of Hk*ceil(capacity/1024)
+ * int32. Replaces compact_positions / _compact_kernel / _compact_dev_kernel
+ * (src/ssa/kernels/labeled_attn.py:166-199; src/ssa/kernels/graph_kernels.py:145-155), with a
+ * deterministic ascending order where the reference's atomics give an arbitrary one. */
+int ssa_compact_positions(const int16_t* labels, int64_t s_lh, const float* w, int64_t s_wr,
+                          int n_heads, int G, int per_head, const int32_t* n_dev, int n_host,
+                          int capacity, int32_t* block_counts, int32_t* idx, int64_t s_ih,
+                          int32_t* cnt, void* stream);
+
+/* ---- cluster index ------------------------------------------------------------------------- */
+
+/* Per-(sequence, KV head) cluster state, all device memory. With layers stacked, every array
+ * holds n_heads = L * heads_per_layer rows. Reference state: SphereIndexGPU._alloc
+ * (src/ssa/attn/sphere_gpu.py:145-164) and SphereIndexFused._alloc (src/ssa/kernels/sphere_fused.py:363-378). */
+typedef struct ssa_index_state {
+  int32_t n_heads, heads_per_layer, C, d, capacity, ms;
+  int32_t summary_bits;     /* 8: scoring/insertion read the int8 copies; 32: the fp32 vectors */
+  int32_t shared_dirs;      /* 1: cent is one [C, d] table shared by all heads (fixed random directions) */
+  int32_t* n_c;             /* [n_heads] clusters in use */
+  float* sum_dir;           /* [n_heads, C, d] sum of member unit directions */
+  int8_t* dir8;             /* [n_heads, C, d] q8(unit(sum_dir)) */
+  float* cent;              /* [n_heads, C, d] unit centroids ([C, d] if shared_dirs) */
+  int8_t* cent8;            /* [n_heads, C, d] q8(unit(cent)) */
+  float* mmax; float* mmin; /* [n_heads, C] longest / shortest centred key */
+  int32_t* count;           /* [n_heads, C] keys per cluster */
+  float* ksum; float* mu_ref;   /* [n_heads, d] running key sum, centring mean */
+  float* rbar; float* cap; float* vthr;   /* [n_heads] */
+  int32_t* flags;           /* [n_heads] bit0 drift, bit1 reset */
+  int32_t* end;             /* [n_heads] binned positions are [1, end) */
+  int32_t* nsplit;          /* [n_heads] splits done in kernels */
+  int16_t* labels;          /* [n_heads, capacity] */
+  int32_t* mem; float* proj; int32_t* side; float* smag;   /* [n_heads, ms] split scratch */
+} ssa_index_state_t;
+
+typedef struct ssa_insert_args {
+  const void* k; int32_t k_dtype; int64_t s_kh; int64_t s_kn;   /* cache of the first layer */
+  const int64_t* koff;       /* [L] element offset of each layer's cache from k; NULL = one layer */
+  const int32_t* n_dev; int32_t n_host;
+  int32_t window; float delta; float capk; int32_t reset_at; int32_t var_min;
+} ssa_insert_args_t;
+
+typedef struct ssa_select_args {
+  const void* q; int32_t q_dtype; int64_t s_qh; int32_t G;
+  float* w; int64_t s_wr;    /* [Hk or Hk*G, C+1]; w[:, C] is set to 1 */
+  double budget;             /* need = ceil(budget * (end - 1)) keys */
+  int32_t group;             /* 0 sum_share, 1 per_head, 2 max, 3 max_rel */
+  float scale;               /* 1/sqrt(d) */
+  int32_t* need_out;         /* optional [Hk] */
+} ssa_select_args_t;
+
+/* Insert the keys that left the recent window since the last call into their nearest cluster
+ * (lowest index on ties), split a cluster that passes its cap in the same kernel, update end,
+ * and set the drift / reset flags; one workgroup per (layer, sequence, KV head).
+ * Replaces _bin_kernel / _bin_dev_kernel / _split_cluster and AllLayerInsert
+ * (src/ssa/kernels/sphere_fused.py:49-227; src/ssa/kernels/graph_kernels.py:63-130,286-325). */
+int ssa_insert(const ssa_index_state_t* st, const ssa_insert_args_t* ins, void* stream);
+
+/* Score every cluster from its summary for the G query heads of each KV head and choose clusters
+ * in decreasing score, ties to the lowest index, until their keys reach the budget; writes w.
+ * With ins non-NULL the insertion of ssa_insert runs first in the same kernel.
+ * Replaces _score_kernel + _pick_kernel / _pick_dev_kernel (src/ssa/kernels/sphere_fused.py:231-313;
+ * src/ssa/kernels/graph_kernels.py:134-141); oracle SphereIndexGPU.labels_and_weights
+ * (src/ssa/attn/sphere_gpu.py:402-442). */
+int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const ssa_select_args_t* sel,
+               void* stream);
+
+/* ---- prefill: fit, bin and summarise the prompt's keys ------------------------------------- */
+
+typedef struct ssa_build_args {
+  const void* k; int32_t k_dtype; int64_t s_kh; int64_t s_kn;   /* [Hk, capacity, d] */
+  const int32_t* heads; int32_t n_sel;   /* heads to (re)build */
+  int32_t start, end;                    /* binned range [start, end) */
+  const float* mu;           /* [n_sel, d] centring mean, or NULL for the mean of the range */
+  float* xn; float* mag;     /* scratch [n_sel, end-start, d] and [n_sel, end-start] */
+  float* sq;                 /* scratch [n_sel, end-start] */
+  int32_t* assign;           /* scratch [n_sel, end-start] */
+  float* part;               /* scratch [n_sel, nblocks, C_fit, d], nblocks = ceil((end-start)/256) */
+  int32_t* part_cnt;         /* scratch [n_sel, nblocks, C_fit] */
+  const int32_t* init_idx;   /* [C_fit] k-means seed members (offsets into the range) */
+  int32_t fit;               /* 1: k-means fit of C_fit clusters first; 0: keep the centroids */
+  int32_t C_fit; int32_t iters;
+} ssa_build_args_t;
+
+/* (Re)build heads: centre, optionally fit cosine k-means (assignment = argmax of the canonical
+ * dot product, lowest index on ties; update = normalised blocked sums), label every key of the
+ * range with its nearest centroid among the first n_c slots and rebuild the summaries and int8
+ * copies. Replaces SphereIndexGPU._build / _bin / spherical_kmeans / _refresh8
+ * (src/ssa/attn/sphere_gpu.py:166-219; src/ssa/attn/clusterkv.py:27-46;
+ * src/ssa/kernels/sphere_fused.py:394-409). */
+int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSA_HIP_H */

@@ -1,0 +1,159 @@
+"""Per-layer decode-step objects for hipGraph capture.
+
+A captured graph replays fixed kernels with fixed arguments, so nothing that changes from one
+decode step to the next may be a host number: the current length ``n`` lives in device memory
+(``n_dev``), each head's binned count in ``end_dev``, and the budget in keys is derived from it
+inside the selection kernel.
+
+Mirrors src/ssa/kernels/graph_kernels.py:
+  * ``DenseAttentionGraph`` (:171-189): exact split-K decode over ``[0, n)``, one launch.
+  * ``SphereIndexGraph`` (:192-279): per step two launches, ``ssa_select`` (insertion of the key
+    that left the window, scoring, selection) and ``ssa_label_attention`` (selection scan,
+    split-K attention over the selected rows, log-sum-exp merge), where the reference issues
+    bin, score, pick, zero, compact, list and merge.
+  * ``AllLayerInsert`` (:286-325): one insertion launch for every layer.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib, stream_ptr
+from .labeled_attn import SplitWork, attn_args, default_splits
+from .sphere_fused import SphereIndexFused
+
+STACKED = ("n_c", "sum_dir", "dir8", "cent", "cent8", "mmax", "mmin", "count", "ksum", "mu_ref", "rbar", "flags",
+           "cap", "vthr", "_mem", "_proj", "_side", "_smag", "nsplit", "labels", "end_dev")
+
+
+class DenseAttentionGraph:
+    """Exact decode attention over ``[0, n)`` with ``n`` in GPU memory (graph-safe)."""
+
+    def __init__(self, *, H: int, H_kv: int, d: int, dtype, device, block_n: int = 32, num_splits: int | None = None):
+        self.G = H // H_kv
+        self.d = d
+        S = num_splits or default_splits(device, H_kv)
+        self.work = SplitWork(H_kv, S, self.G, d, device)
+        self.out = torch.empty(H, d, device=device, dtype=dtype)
+
+    def __call__(self, q, K, V, n_dev):
+        a = attn_args(q, K, V, self.out, self.work, n_dev=n_dev)
+        check(lib().ssa_dense_attention(a, stream_ptr(q.device)), "ssa_dense_attention")
+        return self.out
+
+
+class SphereIndexGraph(SphereIndexFused):
+    """``SphereIndexFused`` for graph capture: ``step`` issues only fixed-argument kernels."""
+
+    def __init__(self, *, budget: float, block_n: int = 32, compact_block: int = 1024, refit_every: int = 0,
+                 num_splits: int | None = None, **kw):
+        super().__init__(**kw)
+        self.refit_every = refit_every
+        self.refits = 0
+        self.budget = budget
+        self.block_n, self.compact_block = block_n, compact_block
+        self.num_splits = num_splits
+
+    def prepare(self, K: torch.Tensor, n: int, H: int) -> None:
+        """Build from the prefilled cache ``K [H_kv, capacity, d]`` holding ``n`` positions (eager,
+        outside the graph) and allocate the step's fixed buffers."""
+        self.observe(K, n)
+        H_kv, d, dev = self.H_kv, self.d, self.device
+        self.G = H // H_kv
+        self.end_dev.fill_(self.end)
+        self.wbuf = torch.zeros(H_kv, self.C + 1, dtype=torch.float32, device=dev)
+        self.wbuf[:, self.C] = 1.0
+        self.need_dev = torch.zeros(H_kv, dtype=torch.int32, device=dev)
+        S = self.num_splits or default_splits(dev, H_kv)
+        self.work = SplitWork(H_kv, S, self.G, d, dev)
+        self.out = torch.empty(H, d, device=dev, dtype=K.dtype)
+
+    def _init(self, K, n):
+        super()._init(K, n)
+        self.end_dev.fill_(self.end)
+
+    def step(self, q, K, V, n_dev, insert: bool = True):
+        """One decode step; ``K, V [H_kv, capacity, d]`` with position ``n - 1`` already written.
+        ``insert=False`` when the keys leaving the window were already inserted for every layer
+        by one launch (``AllLayerInsert``)."""
+        sel = self._select_args(q, self.wbuf, self.budget, "sum_share")
+        sel.need_out = self.need_dev.data_ptr()
+        ins = self._insert_args(K, n_dev=n_dev) if insert else None
+        s = stream_ptr(q.device)
+        check(lib().ssa_select(self._state(), ins, sel, s), "ssa_select")
+        a = attn_args(q, K, V, self.out, self.work, labels=self.labels, w=self.wbuf, n_dev=n_dev)
+        check(lib().ssa_label_attention(a, s), "ssa_label_attention")
+        return self.out
+
+    def _host_end(self) -> None:
+        self.end = int(self.end_dev[0])                          # host sync, only when a flag was set
+
+    def after_replay(self, K: torch.Tensor) -> None:
+        """Between replays: every ``check_every`` steps read the drift flags without a sync; once
+        a copy has landed, recentre the flagged heads (eager, in place)."""
+        self.head_steps += self.H_kv
+        self._steps += 1
+        if self.refit_every and self._steps % self.refit_every == 0:
+            self._refit(K)
+        elif self._steps % self.check_every == 0:
+            self._check_flags(K)
+
+    def _refit(self, K: torch.Tensor) -> None:
+        """Fit the clusters again on every binned key, with a fresh mean."""
+        self._host_end()
+        self.fitted = [False] * self.H_kv
+        self.n_c.fill_(self.C_init)
+        self._build(K, torch.arange(self.H_kv), None)
+        self._split_after_fit(K)
+        self.flags.zero_()
+        self._pending = None
+        self.refits += 1
+
+    def _build_heads(self, K, heads, mu, fit):
+        super()._build_heads(K, heads, mu, fit)
+        self.end_dev[torch.tensor(heads, device=self.device).long()] = self.end
+
+
+class AllLayerInsert:
+    """One insertion launch for every layer. The key that leaves the recent window at a step was
+    written ``window`` steps earlier at every layer, so all layers' insertions (and the splits
+    they trigger) run together, one workgroup per (layer, KV head).
+
+    Built after every layer's index is prepared: each per-head state array of all layers is
+    moved into one array stacked over layers and every layer's index is pointed at its slice,
+    so per-layer kernels and host-side maintenance keep working on the same memory."""
+
+    def __init__(self, layers: list, caches: list):
+        first = layers[0]
+        if first.window < 1:
+            raise AssertionError("with no recent window the key to insert is not yet written at later layers")
+        if not all(i.H_kv == first.H_kv and i.end == first.end for i in layers):
+            raise AssertionError("layers must share the head count and the binned length")
+        self.layers, self.L = layers, len(layers)
+        big = {}
+        for name in STACKED:
+            t0 = getattr(first, name, None)
+            if t0 is None:
+                continue
+            if name == "cent" and first.partition != "kmeans":
+                continue                                        # one shared table
+            big[name] = torch.stack([getattr(i, name) for i in layers])
+            for l, i in enumerate(layers):
+                setattr(i, name, big[name][l])
+        self.big = big
+        first._stacked = big
+        k0 = caches[0]
+        size = k0.element_size()
+        off = [k.data_ptr() - k0.data_ptr() for k in caches]
+        if not (all(o % size == 0 for o in off) and all(k.stride() == k0.stride() for k in caches)):
+            raise AssertionError("layer caches must share strides")
+        self.koff = torch.tensor([o // size for o in off], dtype=torch.int64, device=first.device)
+        self.k0 = k0
+
+    def __call__(self, n_dev) -> None:
+        f = self.layers[0]
+        st = f._state(layers=self.L)
+        if f.partition != "kmeans":
+            st.cent = f.cent.data_ptr()
+        check(lib().ssa_insert(st, f._insert_args(self.k0, n_dev=n_dev, koff=self.koff), stream_ptr(f.device)),
+              "ssa_insert")
