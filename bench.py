@@ -1,0 +1,299 @@
+"""Benchmark of the hot path: one layer's clustered sparse decode-attention step on one MI355X.
+
+Workload: batch 1, 16 query heads / 8 KV heads, head_dim 128, bf16
+KV cache, context 32768, keys from the synthetic mixture-of-directions distribution
+(ssa_amd.synth), 256 k-means clusters per KV head (10 iterations), window 64, budgets 5 / 10 /
+20 / 40 %, each against the same GPU's dense split-K decode over the full cache.
+
+A step is what the reference's graph decoder runs per layer and token
+(src/ssa/kernels/graph_kernels.py:220-244): insertion of the key leaving the recent window,
+cluster scoring and selection (one kernel, ssa_select), then split-K attention over the
+selected rows with the log-sum-exp merge (one kernel, ssa_label_attention); both are captured
+in a hipGraph. Timing follows the reference's harness (src/ssa/harness/kernel_bench.py:34-49,
+165-214) with two changes for MI355X: events bracket each replay with work queued ahead (no
+host gap inside a measurement), and replays rotate over ROT independent caches (ROT x 134 MB,
+well above the 256 MB Infinity Cache) so every step reads its K/V rows from HBM.
+
+Bytes per step follow the reference's accounting (src/ssa/attn/accounting.py:19-32) per
+(sequence, KV head): selected K+V rows 2*rows*d*2, label scan 2n, 6 B per row read, summaries
+C*(d+12) and centroids C*d (8-bit), inserted key 2d and its cluster's fp32 sum 8d. The roofline
+entry is the attention kernel alone: its algorithmic bytes (K+V rows + labels) over its own
+event-timed duration.
+
+The CPU baseline times the oracle's numpy restatement of the reference's CPU path
+(SphereIndexRef: observe one key, labels_and_weights, label_weighted_attention) at the same
+shape in fp32, on a bounded number of steps.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]; prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "sparse-kv-reads_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+H, H_KV, D, N, C, WINDOW = 16, 8, 128, 32768, 256, 64
+BUDGETS = (0.05, 0.10, 0.20, 0.40)
+HEADLINE = 0.20
+PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def step_bytes(rows_per_head, n, *, d=D, C=C, summary_bits=8):
+    """Reference accounting (src/ssa/attn/accounting.py:19-32) summed over KV heads."""
+    vec = d * summary_bits / 8
+    tot = 0.0
+    for r in rows_per_head:
+        tot += 2 * r * d * 2 + C * (vec + 12) + C * vec + 2 * n + 6 * r + 2 * d + 8 * d
+    return tot
+
+
+def attn_bytes(rows_per_head, n, *, d=D, C=C):
+    """What the fused selection + attention kernel must read per launch: the selected K and V
+    rows, the label scan and, once per head, the cluster summaries it scores (int8 direction,
+    two fp32 lengths, an int32 count)."""
+    return float(sum(2 * r * d * 2 + 2 * n + C * (d + 12) for r in rows_per_head))
+
+
+class Set:
+    """One independent (cache, index) pair; its length lives in ``n_dev`` (a slice of one
+    tensor shared by all sets, so one launch advances every set)."""
+
+    def __init__(self, seed, n, extra, splits, device, n_dev):
+        import torch
+        from ssa_amd.graph_kernels import DenseAttentionGraph, SphereIndexGraph
+        from ssa_amd.synth import make_cache
+        cap = n + extra
+        K, V, q, _ = make_cache(1, H_KV, cap, D, H=H, centers=C, capacity=cap, seed=seed, dtype=torch.bfloat16,
+                                device=device, gen_device=str(device))
+        self.K, self.V, self.q = K[0], V[0], q[0].contiguous()
+        self.n_dev = n_dev
+        t = time.time()
+        self.idx = SphereIndexGraph(budget=HEADLINE, C=C, window=WINDOW, delta=0.03, capacity=cap,
+                                    check_every=10 ** 9, partition="kmeans", num_splits=splits)
+        self.idx.prepare(self.K, n, H)
+        torch.cuda.synchronize()
+        self.prefill_s = time.time() - t
+        self.dense = DenseAttentionGraph(H=H, H_kv=H_KV, d=D, dtype=torch.bfloat16, device=device,
+                                         num_splits=splits)
+
+
+def capture(fns):
+    """One graph running ``fns`` in order (each one layer-step on its own cache)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    return g
+
+
+def time_graph(g, reps, per, *, advance=None):
+    """Median microseconds per step over ``reps`` replays of graph ``g`` holding ``per`` steps.
+    Replays are queued back to back (the GPU never waits on the host inside a measurement);
+    ``advance`` (one small kernel, between replays) moves every cache to its next position."""
+    import torch
+    ev = []
+    for _ in range(reps):
+        if advance is not None:
+            advance()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        ev.append((a, b))
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 / per for a, b in ev[1:])
+    return us[len(us) // 2], sum(us) / len(us)
+
+
+def cpu_baseline(seconds: float):
+    """The oracle's numpy restatement of the reference CPU path at the config-1 shape (fp32):
+    per step one key observed, labels_and_weights, label_weighted_attention."""
+    import numpy as np
+    import torch
+    from oracle.reference import SphereIndexRef
+    from ssa_amd.sphere_fused import kmeans_init_indices
+    from ssa_amd.synth import make_cache
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:
+        threads = 1
+    K, V, q, _ = make_cache(1, H_KV, N + 64, D, H=H, centers=C, seed=0, dtype=torch.float32)
+    K, V, q = K[0].numpy(), V[0].numpy(), q[0].numpy()
+    ref = SphereIndexRef(C=C, window=WINDOW, init_indices=lambda m, c, s: kmeans_init_indices(m, c, s).numpy())
+    t0 = time.time()
+    ref.observe(K, N)
+    prefill = time.time() - t0
+    times, rows = [], []
+    n = N
+    t_end = time.time() + seconds
+    while time.time() < t_end and n < N + 64:
+        n += 1
+        t = time.time()
+        out, labels, w = ref.attend(q, K, V, n=n, budget=HEADLINE, fast=True)
+        times.append(time.time() - t)
+        rows = [int((w[h][labels[h].astype(np.int64)] > 0).sum()) for h in range(H_KV)]
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": step_bytes(rows, n) / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_step": med * 1e6, "prefill_s": prefill,
+            "sample": f"{len(times)} decode steps at n={N}..{n}, fp32, B=1, 16/8 heads, d=128, C=256, "
+                      f"budget {HEADLINE}, after one k-means prefill ({prefill:.1f} s); median step",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--rot", type=int, default=16, help="independent caches; one graph steps through all of them")
+    ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: four workgroups per CU)")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU: the clustered sparse decode step of one "
+                                   "GPU's share is the measured unit; multi-GPU sharding is described in DESIGN.md "
+                                   "and not run"}))
+        return 2
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    splits = args.splits or None
+    reps = max(args.steps // args.rot, 4)
+    extra = (args.warmup + 3) * len(BUDGETS) + reps * (len(BUDGETS) + 1) + 64
+    n_all = torch.full((args.rot,), N, dtype=torch.int32, device=dev)
+    log(f"building {args.rot} caches of {N} tokens ...")
+    sets = [Set(s, N, extra, splits, dev, n_all[s:s + 1]) for s in range(args.rot)]
+    log(f"prefill (k-means fit, binning, summaries) per cache: {sets[0].prefill_s:.3f} s (first), "
+        f"{sets[-1].prefill_s:.3f} s (last)")
+    advance = lambda: n_all.add_(1)                                   # noqa: E731
+
+    graphs = {"dense": capture([lambda st=st: st.dense(st.q, st.K, st.V, st.n_dev) for st in sets])}
+    graphs["insert"] = capture([lambda st=st: _insert_only(st) for st in sets])
+    for b in BUDGETS:
+        for st in sets:
+            st.idx.budget = b
+        graphs[("step", b)] = capture([lambda st=st: st.idx.step(st.q, st.K, st.V, st.n_dev) for st in sets])
+        graphs[("attn", b)] = capture([lambda st=st: _fused_only(st) for st in sets])
+    for st in sets:
+        st.idx.budget = HEADLINE
+
+    res = {}
+    R = args.rot
+    for b in BUDGETS:
+        time_graph(graphs[("step", b)], args.warmup, R, advance=advance)
+        res[("step", b)] = time_graph(graphs[("step", b)], reps, R, advance=advance)
+        res[("attn", b)] = time_graph(graphs[("attn", b)], reps, R)
+        res[("rows", b)] = sets[-1].idx.work.cnt.tolist()      # rows read per head, counted by the kernel
+    res["insert"] = time_graph(graphs["insert"], reps, R, advance=advance)
+    time_graph(graphs["dense"], 3, R)
+    res["dense"] = time_graph(graphs["dense"], reps, R)
+
+    # the timed region: exactly K steps at the headline budget (K/rot replays of the rot-step
+    # graph), bracketed by synchronisations
+    g = graphs[("step", HEADLINE)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        advance()
+        g.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    steps_timed = reps * R
+    n_now = int(n_all[0])
+
+    dense_us = res["dense"][0]
+    detail = {}
+    for b in BUDGETS:
+        rows = res[("rows", b)]
+        step_us, attn_us = res[("step", b)][0], res[("attn", b)][0]
+        detail[f"{int(b * 100)}%"] = {
+            "step_us": round(step_us, 2), "select_attention_us": round(attn_us, 2),
+            "rows_per_head": int(sum(rows) / len(rows)),
+            "step_effective_GBs": round(step_bytes(rows, N) / step_us / 1e3, 1),
+            "attention_GBs": round(attn_bytes(rows, N) / attn_us / 1e3, 1),
+            "speedup_vs_dense": round(dense_us / step_us, 2)}
+    rows20 = res[("rows", HEADLINE)]
+    head = detail[f"{int(HEADLINE * 100)}%"]
+    attn_mean = res[("attn", HEADLINE)][1]
+    achieved = attn_bytes(rows20, N) / attn_mean / 1e3
+    out = {
+        "metric": "sparse decode-attn effective HBM GB/s @32k ctx 20% budget (reference byte accounting, "
+                  "per-layer graph step: insert+score+pick+attention)",
+        "value": head["step_effective_GBs"], "unit": "GB/s", "n_gpus": 1, "steps": steps_timed,
+        "warmup": args.warmup, "ms_per_step": round(wall / steps_timed * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (mixture-of-directions keys, N(0,1) values; ssa_amd.synth)",
+        "config": {"workload": "configs[1]: one layer, B=1, 16 q / 8 kv heads, d=128, bf16 cache, ctx 32768, "
+                               "256 k-means clusters, window 64", "batch": 1, "context": N, "heads": [H, H_KV],
+                   "head_dim": D, "clusters": C, "budgets": list(BUDGETS), "rotation_caches": args.rot,
+                   "splits": sets[0].idx.work.S, "context_at_end": n_now},
+        "detail": {**detail, "insert_us": round(res["insert"][0], 2), "dense_us": round(dense_us, 2),
+                   "dense_GBs": round(2 * H_KV * N * D * 2 / dense_us / 1e3, 1),
+                   "prefill_s": round(sets[-1].prefill_s, 4)},
+        "roofline": {"bound": "hbm", "kernel": "ssa_sparse_step (decode_kernel, fused selection)",
+                     "achieved": round(achieved, 1),
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": attn_bytes(rows20, N), "avg_launch_us": round(attn_mean, 3)},
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def _fused_only(st):
+    """The fused selection + attention launch of one step (no insertion)."""
+    from ssa_amd._lib import check, lib, stream_ptr
+    from ssa_amd.labeled_attn import attn_args
+    idx = st.idx
+    sel = idx._select_args(st.q, idx.wbuf, idx.budget, "sum_share")
+    a = attn_args(st.q, st.K, st.V, idx.out, idx.work, labels=idx.labels, w=idx.wbuf, n_dev=st.n_dev)
+    check(lib().ssa_sparse_step(idx._state(), sel, a, stream_ptr(st.q.device)), "ssa_sparse_step")
+
+
+def _insert_only(st):
+    """The insertion launch of one step."""
+    from ssa_amd._lib import check, lib, stream_ptr
+    idx = st.idx
+    check(lib().ssa_insert(idx._state(), idx._insert_args(st.K, n_dev=st.n_dev), stream_ptr(st.q.device)),
+          "ssa_insert")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

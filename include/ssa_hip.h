@@ -128,6 +128,15 @@ int ssa_insert(const ssa_index_state_t* st, const ssa_insert_args_t* ins, void* 
 int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const ssa_select_args_t* sel,
                void* stream);
 
+/* One layer's decode step after insertion, in one launch: every workgroup of the attention grid
+ * computes its head's selection exactly as ssa_select does (same bits, from the index state and
+ * sel), then attends over the selected rows as ssa_label_attention does. args->labels must be
+ * st->labels; sel->w, if non-NULL, receives the selection (written by one workgroup per head).
+ * Replaces the per-layer score + pick + compact + list + merge launches of
+ * SphereIndexGraph.step (src/ssa/kernels/graph_kernels.py:220-244). */
+int ssa_sparse_step(const ssa_index_state_t* st, const ssa_select_args_t* sel, const ssa_attn_args_t* args,
+                    void* stream);
+
 /* ---- prefill: fit, bin and summarise the prompt's keys ------------------------------------- */
 
 typedef struct ssa_build_args {

@@ -54,6 +54,26 @@ def label_weighted_attention(q, K, V, labels, w):
     return np.einsum("hn,hnd->hd", A, Vx)
 
 
+def label_weighted_attention_f32(q, K, V, labels, w):
+    """The same quantity in float32 with BLAS products per KV head (the reference computes in
+    float32 for bf16 / fp32 caches, src/ssa/attn/geometry.py:20-24); shared ``w [H_kv, L]`` only."""
+    q = np.asarray(q, np.float32)
+    H, d = q.shape
+    H_kv, n, _ = K.shape
+    G = H // H_kv
+    out = np.empty((H, d), np.float32)
+    scale = np.float32(1.0 / math.sqrt(d))
+    for h in range(H_kv):
+        wr = np.asarray(w, np.float32)[h][np.asarray(labels[h, :n], np.int64)]
+        sel = np.nonzero(wr > 0)[0]                                          # only these rows are read
+        s = (K[h, sel] @ q[h * G:(h + 1) * G].T) * scale + np.log(wr[sel])[:, None]    # [rows, G]
+        s = s - s.max(0, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(0, keepdims=True)
+        out[h * G:(h + 1) * G] = p.T @ V[h, sel]
+    return out
+
+
 def dense(q, K, V):
     """Exact ``softmax(q K^T / sqrt(d)) V`` with ``K, V [H_kv, n, d]`` -> ``[H, d]`` (float64)."""
     H_kv, n, _ = np.shape(K)
@@ -183,14 +203,14 @@ def spherical_kmeans(X: np.ndarray, *, C: int, iters: int = 10, init: np.ndarray
     cent = Xn[:, init].copy()
     assign = None
     for _ in range(iters):
-        assign = np.einsum("hmd,hcd->hmc", Xn, cent).argmax(-1)
+        assign = np.matmul(Xn, cent.transpose(0, 2, 1)).argmax(-1)
         sums = np.zeros((h, C, d), X.dtype)
         cnt = np.zeros((h, C), np.int64)
         for i in range(h):
             np.add.at(sums[i], assign[i], Xn[i])
             np.add.at(cnt[i], assign[i], 1)
         cent = np.where((cnt > 0)[..., None], normalize(sums), cent)
-    assign = np.einsum("hmd,hcd->hmc", Xn, cent).argmax(-1)
+    assign = np.matmul(Xn, cent.transpose(0, 2, 1)).argmax(-1)
     return assign, cent
 
 
@@ -244,7 +264,7 @@ class SphereIndexRef:
     def _bin(self, Kr: np.ndarray, p0: int) -> None:
         mag = np.linalg.norm(Kr, axis=-1)
         Kn = Kr / np.maximum(mag, 1e-12)[..., None]
-        lab = np.einsum("hmd,hcd->hmc", Kn, self.cent).argmax(-1)
+        lab = np.matmul(Kn, self.cent.transpose(0, 2, 1)).argmax(-1)
         for h in range(Kr.shape[0]):
             np.add.at(self.sum_dir[h], lab[h], Kn[h])
             np.maximum.at(self.mmax[h], lab[h], mag[h])
@@ -271,7 +291,8 @@ class SphereIndexRef:
                                nb=self.end - self.start, budget=budget)
         return self.labels[:, :n], w
 
-    def attend(self, q, K, V, *, n: int, budget: float):
+    def attend(self, q, K, V, *, n: int, budget: float, fast: bool = False):
         self.observe(K, n)
         labels, w = self.labels_and_weights(q, n=n, budget=budget)
-        return label_weighted_attention(q, K[:, :n], V[:, :n], labels, w), labels, w
+        f = label_weighted_attention_f32 if fast else label_weighted_attention
+        return f(q, K[:, :n], V[:, :n], labels, w), labels, w

@@ -18,16 +18,12 @@
 //
 // One workgroup owns one (layer, sequence, KV head) for insertion and selection, so every
 // summary has a single writer and no float atomics are needed.
-#include "ssa_common.h"
-#include "../../include/ssa_hip.h"
+#include "select.h"
 
 namespace ssa {
 
 constexpr int kT = 256;       // threads per workgroup
 constexpr int kW = kT / 64;   // waves
-constexpr int kMaxD = 256;
-constexpr int kMaxC = 1024;
-constexpr int kMaxG = 8;
 constexpr int kTile = 16;     // member rows staged in LDS by the split's ordered sums
 constexpr int kKB = 256;      // keys per block of the prefill's blocked sums
 
@@ -46,13 +42,7 @@ struct IndexSmem {
   float scal[4];
   int scali[4];
   union {
-    struct {
-      float q[kMaxG][kMaxD];
-      float z[kMaxG][kMaxC];
-      float key[kMaxC];
-      int cnt[kMaxC];
-      float tree[kMaxC];
-    } sel;
+    SelSmem<kMaxG> sel;
     struct {
       float tile[kTile][kMaxD];
       int tside[kTile];
@@ -108,46 +98,24 @@ __device__ int block_sum_i(IndexSmem& S, int v) {
 
 // Canonical unit vector of an LDS vector x (d entries) written to y (may alias x).
 __device__ void block_unit(IndexSmem& S, const float* x, float* y, int d) {
-  if (threadIdx.x == 0) S.scal[3] = fmaxf(sqrtf(cdot_ptr(x, x, d)), 1e-12f);
+  if (threadIdx.x < 64) {
+    const float r = fmaxf(sqrtf(wave_cdot(x, x, d)), 1e-12f);
+    if (threadIdx.x == 0) S.scal[3] = r;
+  }
   __syncthreads();
   const float r = S.scal[3];
   if (threadIdx.x < d) y[threadIdx.x] = x[threadIdx.x] / r;
   __syncthreads();
 }
 
-// ---- head views --------------------------------------------------------------------------
-
-struct Head {
-  int C, d, ms;
-  float* sum_dir; int8_t* dir8; float* cent; int8_t* cent8;
-  float* mmax; float* mmin; int32_t* count; int16_t* labels;
-  int32_t* mem; float* proj; int32_t* side; float* smag;
-  bool q8dirs;    // scoring reads dir8
-  bool q8cent;    // insertion reads cent8
+// Key rows of one head's cache, element type T: element i of position p.
+template <typename T>
+struct KeysT {
+  const T* base; int64_t s_kn;
+  __device__ __forceinline__ float operator()(int p, int i) const { return to_f32(base[(int64_t)p * s_kn + i]); }
 };
 
-__device__ Head head_view(const ssa_index_state_t& st, int h) {
-  Head H;
-  H.C = st.C; H.d = st.d; H.ms = st.ms;
-  const int64_t cd = (int64_t)st.C * st.d;
-  H.sum_dir = st.sum_dir + h * cd;
-  H.dir8 = st.dir8 ? st.dir8 + h * cd : nullptr;
-  H.cent = st.shared_dirs ? st.cent : st.cent + h * cd;
-  H.cent8 = st.cent8 ? st.cent8 + h * cd : nullptr;
-  H.mmax = st.mmax + (int64_t)h * st.C;
-  H.mmin = st.mmin + (int64_t)h * st.C;
-  H.count = st.count + (int64_t)h * st.C;
-  H.labels = st.labels + (int64_t)h * st.capacity;
-  H.mem = st.mem + (int64_t)h * st.ms;
-  H.proj = st.proj + (int64_t)h * st.ms;
-  H.side = st.side + (int64_t)h * st.ms;
-  H.smag = st.smag + (int64_t)h * st.ms;
-  H.q8dirs = st.summary_bits == 8 && st.dir8;
-  H.q8cent = st.summary_bits == 8 && !st.shared_dirs && st.cent8;
-  return H;
-}
-
-// Key rows of one head's cache: element i of position p.
+// Key rows of one head's cache, element type given at run time: element i of position p.
 struct Keys {
   const char* base; int dt; int64_t s_kn;
   __device__ float operator()(int p, int i) const { return load_as_f32(base, dt, (int64_t)p * s_kn + i); }
@@ -307,10 +275,11 @@ __device__ void split_cluster(IndexSmem& S, const ssa_index_state_t& st, const H
 
 // ---- insertion ---------------------------------------------------------------------------
 
+template <int D>
 __device__ void insert_phase(IndexSmem& S, const IndexArgs& A, int h) {
   const ssa_index_state_t& st = A.st;
   const ssa_insert_args_t& in = A.ins;
-  const int tid = threadIdx.x, d = st.d, C = st.C;
+  const int tid = threadIdx.x, wave = tid >> 6, C = st.C;
   const Head H = head_view(st, h);
   const int n = in.n_dev ? *in.n_dev : in.n_host;
   const int old_end = st.end[h];
@@ -323,63 +292,64 @@ __device__ void insert_phase(IndexSmem& S, const IndexArgs& A, int h) {
   K.base = reinterpret_cast<const char*>(in.k) +
            (int64_t)elem_size(in.k_dtype) * ((in.koff ? in.koff[layer] : 0) + (int64_t)(h % hpl) * in.s_kh);
   float mu_i = 0.f, ks_i = 0.f;
-  if (tid < d) {
-    mu_i = st.mu_ref[(int64_t)h * d + tid];
-    ks_i = st.ksum[(int64_t)h * d + tid];
+  if (tid < D) {
+    mu_i = st.mu_ref[(int64_t)h * D + tid];
+    ks_i = st.ksum[(int64_t)h * D + tid];
     S.mu[tid] = mu_i;
   }
   int n_act = st.n_c[h];
   const float cap = st.cap[h], vthr = st.vthr[h];
   __syncthreads();
   for (int p = old_end; p < new_end && n_act > 0; ++p) {
-    if (tid < d) {
+    if (tid < D) {
       const float kv = K(p, tid);
       ks_i = ks_i + kv;
       S.kr[tid] = kv - mu_i;
     }
     __syncthreads();
-    if (tid == 0) S.scal[0] = sqrtf(cdot_ptr(S.kr, S.kr, d));
+    if (wave == 0) {
+      const float mag = sqrtf(wave_cdot(S.kr, S.kr, D));
+      if (tid == 0) S.scal[0] = mag;
+    }
     __syncthreads();
     const float mag = S.scal[0];
     const float magc = fmaxf(mag, 1e-12f);
-    if (tid < d) S.kn[tid] = S.kr[tid] / magc;
+    if (tid < D) S.kn[tid] = S.kr[tid] / magc;
     __syncthreads();
     float best = 0.f;
     int bi = -1;
     for (int c = tid; c < n_act; c += kT) {
-      float sc;
-      if (H.q8cent) {
-        const int8_t* r = H.cent8 + (int64_t)c * d;
-        sc = cdot([&](int i) { return (float)r[i]; }, [&](int i) { return S.kn[i]; }, d);
-      } else {
-        const float* r = H.cent + (int64_t)c * d;
-        sc = cdot([&](int i) { return r[i]; }, [&](int i) { return S.kn[i]; }, d);
-      }
+      float x[D];
+      if (H.q8cent) load_row<D>(H.cent8 + (int64_t)c * D, x);
+      else load_row<D>(H.cent + (int64_t)c * D, x);
+      const float sc = cdot([&](int i) { return x[i]; }, [&](int i) { return S.kn[i]; }, D);
       argmax_merge(best, bi, sc, c);
     }
     block_argmax(S, best, bi);
     const int row = bi;
-    if (tid < d) {
-      const float sd = H.sum_dir[(int64_t)row * d + tid] + S.kn[tid];
-      H.sum_dir[(int64_t)row * d + tid] = sd;
+    if (tid < D) {
+      const float sd = H.sum_dir[(int64_t)row * D + tid] + S.kn[tid];
+      H.sum_dir[(int64_t)row * D + tid] = sd;
       S.sd[tid] = sd;
     }
     __syncthreads();
-    if (tid == 0) {
-      const float sdsq = cdot_ptr(S.sd, S.sd, d);
-      S.scal[1] = sqrtf(sdsq);
-      H.mmax[row] = fmaxf(H.mmax[row], mag);
-      H.mmin[row] = fminf(H.mmin[row], mag);
-      const int cn = H.count[row] + 1;
-      H.count[row] = cn;
-      H.labels[p] = (int16_t)row;
-      const float cnf = (float)cn;
-      const bool wide = (1.0f - sdsq / (cnf * cnf) > vthr) && (cn >= in.var_min);
-      const bool over = cnf > fmaxf(cap, in.capk * (float)p);
-      S.scali[0] = ((over || wide) && n_act < C && cn >= 2 && cn <= H.ms) ? 1 : 0;
+    if (wave == 0) {
+      const float sdsq = wave_cdot(S.sd, S.sd, D);
+      if (tid == 0) {
+        S.scal[1] = sqrtf(sdsq);
+        H.mmax[row] = fmaxf(H.mmax[row], mag);
+        H.mmin[row] = fminf(H.mmin[row], mag);
+        const int cn = H.count[row] + 1;
+        H.count[row] = cn;
+        H.labels[p] = (int16_t)row;
+        const float cnf = (float)cn;
+        const bool wide = (1.0f - sdsq / (cnf * cnf) > vthr) && (cn >= in.var_min);
+        const bool over = cnf > fmaxf(cap, in.capk * (float)p);
+        S.scali[0] = ((over || wide) && n_act < C && cn >= 2 && cn <= H.ms) ? 1 : 0;
+      }
     }
     __syncthreads();
-    if (H.dir8 && tid < d) H.dir8[(int64_t)row * d + tid] = q8(S.sd[tid] / fmaxf(S.scal[1], 1e-12f));
+    if (H.dir8 && tid < D) H.dir8[(int64_t)row * D + tid] = q8(S.sd[tid] / fmaxf(S.scal[1], 1e-12f));
     if (S.scali[0]) {
       __syncthreads();
       split_cluster(S, st, H, K, h, row, n_act, p + 1);
@@ -389,152 +359,61 @@ __device__ void insert_phase(IndexSmem& S, const IndexArgs& A, int h) {
   }
   // running mean vs the centring mean: drift flag; cluster count: reset flag
   const float nb = (float)(new_end - 1);
-  if (tid < d) {
-    st.ksum[(int64_t)h * d + tid] = ks_i;
+  if (tid < D) {
+    st.ksum[(int64_t)h * D + tid] = ks_i;
     S.vs[tid] = ks_i / fmaxf(nb, 1.f) - mu_i;
   }
   __syncthreads();
-  if (tid == 0) {
-    const float dist = sqrtf(cdot_ptr(S.vs, S.vs, d));
-    const bool moved = (dist > in.delta * st.rbar[h]) && (nb > 0.f);
-    st.flags[h] = st.flags[h] | (moved ? 1 : 0) | ((n_act >= in.reset_at) ? 2 : 0);
-    st.end[h] = new_end;
-    S.scali[2] = new_end;
+  if (wave == 0) {
+    const float dist = sqrtf(wave_cdot(S.vs, S.vs, D));
+    if (tid == 0) {
+      const bool moved = (dist > in.delta * st.rbar[h]) && (nb > 0.f);
+      st.flags[h] = st.flags[h] | (moved ? 1 : 0) | ((n_act >= in.reset_at) ? 2 : 0);
+      st.end[h] = new_end;
+      S.scali[2] = new_end;
+    }
   }
   __syncthreads();
 }
 
 // ---- selection -----------------------------------------------------------------------------
 
-// Take cluster c iff it is live and the live clusters ranked before it, by (key desc, index
-// asc), hold fewer than `need` keys.
-__device__ void rank_take(IndexSmem& S, const float* key, int n_act, int C, int64_t need, float* wrow) {
-  for (int c = threadIdx.x; c < C; c += kT) {
-    const bool live = c < n_act && S.u.sel.cnt[c] > 0;
-    int64_t before = 0;
-    if (live) {
-      const float kc = key[c];
-      for (int j = 0; j < n_act; ++j) {
-        const float kj = key[j];
-        before += (kj > kc || (kj == kc && j < c)) ? S.u.sel.cnt[j] : 0;
-      }
-    }
-    wrow[c] = (live && before < need) ? 1.f : 0.f;
-  }
-}
-
+template <int D>
 __device__ void select_phase(IndexSmem& S, const IndexArgs& A, int h, int end) {
   const ssa_index_state_t& st = A.st;
   const ssa_select_args_t& sl = A.sel;
-  const int tid = threadIdx.x, d = st.d, C = st.C, G = sl.G;
+  const int tid = threadIdx.x, G = sl.G;
   const Head H = head_view(st, h);
-  const bool per_head = sl.group == 1;
-  const int nrows = per_head ? G : 1;
-  const int nb = end - 1;
-  const double needd = nb > 0 ? ceil(sl.budget * (double)nb) : 0.0;
-  const int64_t need = needd > 9.0e18 ? (int64_t)9e18 : (int64_t)needd;
-  if (sl.need_out && tid == 0) sl.need_out[h] = (int32_t)min(need, (int64_t)INT32_MAX);
-  for (int r = 0; r < nrows; ++r) {
-    float* wrow = sl.w + (int64_t)(per_head ? h * G + r : h) * sl.s_wr;
-    if (tid == 0) wrow[C] = 1.f;
-    if (nb <= 0 || need <= 0)
-      for (int c = tid; c < C; c += kT) wrow[c] = 0.f;
-  }
-  if (nb <= 0 || need <= 0) return;
   const int n_act = st.n_c[h];
-  for (int e = tid; e < G * d; e += kT) {
-    const int g = e / d, i = e % d;
+  const bool per_head = sl.group == 1;
+  if (sl.need_out && tid == 0) {
+    const int nb = end - 1;
+    const double need = nb > 0 ? ceil(sl.budget * (double)nb) : 0.0;
+    sl.need_out[h] = (int32_t)fmin(need, 2147483647.0);
+  }
+  for (int e = tid; e < G * D; e += kT) {
+    const int g = e / D, i = e % D;
     S.u.sel.q[g][i] = load_as_f32(sl.q, sl.q_dtype, (int64_t)(h * G + g) * sl.s_qh + i);
   }
   __syncthreads();
-  for (int c = tid; c < C; c += kT) {
-    const bool live = c < n_act && H.count[c] > 0;
-    S.u.sel.cnt[c] = live ? H.count[c] : 0;
-    if (live) {
-      float nrm, dots[kMaxG];
-      if (H.q8dirs) {
-        const int8_t* r = H.dir8 + (int64_t)c * d;
-        auto dv = [&](int i) { return (float)r[i]; };
-        nrm = fmaxf(sqrtf(cdot(dv, dv, d)), 1e-12f);
-        for (int g = 0; g < G; ++g) dots[g] = cdot([&](int i) { return S.u.sel.q[g][i]; }, dv, d);
-      } else {
-        const float* r = H.sum_dir + (int64_t)c * d;
-        auto dv = [&](int i) { return r[i]; };
-        nrm = fmaxf(sqrtf(cdot(dv, dv, d)), 1e-12f);
-        for (int g = 0; g < G; ++g) dots[g] = cdot([&](int i) { return S.u.sel.q[g][i]; }, dv, d);
-      }
-      const float mx = H.mmax[c], mn = H.mmin[c];
-      for (int g = 0; g < G; ++g) {
-        const float p = dots[g] / nrm;
-        const float e = p >= 0.f ? mx * p : mn * p;
-        S.u.sel.z[g][c] = per_head ? e : e * sl.scale;
-      }
-    } else {
-      for (int g = 0; g < G; ++g) S.u.sel.z[g][c] = -INFINITY;
-    }
-  }
-  __syncthreads();
-  if (per_head) {
-    for (int g = 0; g < G; ++g)
-      rank_take(S, S.u.sel.z[g], n_act, C, need, sl.w + (int64_t)(h * G + g) * sl.s_wr);
-    return;
-  }
-  if (sl.group == 0) {
-    // sum_share: per head a softmax over live clusters, summed over the heads
-    for (int g = 0; g < G; ++g) {
-      float zm = -INFINITY;
-      for (int c = tid; c < C; c += kT) zm = fmaxf(zm, S.u.sel.z[g][c]);
-      zm = block_max(S, zm);
-      for (int c = tid; c < C; c += kT) {
-        const float ex = S.u.sel.cnt[c] > 0 ? cexp(S.u.sel.z[g][c] - zm) : 0.f;
-        S.u.sel.z[g][c] = ex;
-        S.u.sel.tree[c] = ex;
-      }
-      __syncthreads();
-      for (int half = C >> 1; half >= 1; half >>= 1) {
-        for (int c = tid; c < half; c += kT) S.u.sel.tree[c] = S.u.sel.tree[c] + S.u.sel.tree[c + half];
-        __syncthreads();
-      }
-      if (tid == 0) S.scal[2] = S.u.sel.tree[0];
-      __syncthreads();
-      const float tot = S.scal[2];
-      for (int c = tid; c < C; c += kT) S.u.sel.z[g][c] = S.u.sel.z[g][c] / tot;
-      __syncthreads();
-    }
-    for (int c = tid; c < C; c += kT) {
-      float s = 0.f;
-      for (int g = 0; g < G; ++g) s = s + S.u.sel.z[g][c];
-      S.u.sel.key[c] = S.u.sel.cnt[c] > 0 ? s : -INFINITY;
-    }
-  } else {
-    // max / max_rel
-    float zmx[kMaxG];
-    for (int g = 0; g < G; ++g) {
-      float zm = -INFINITY;
-      for (int c = tid; c < C; c += kT) zm = fmaxf(zm, S.u.sel.z[g][c]);
-      zmx[g] = sl.group == 3 ? block_max(S, zm) : 0.f;
-    }
-    for (int c = tid; c < C; c += kT) {
-      float s = -INFINITY;
-      for (int g = 0; g < G; ++g) s = fmaxf(s, S.u.sel.z[g][c] - zmx[g]);
-      S.u.sel.key[c] = S.u.sel.cnt[c] > 0 ? s : -INFINITY;
-    }
-  }
-  __syncthreads();
-  rank_take(S, S.u.sel.key, n_act, C, need, sl.w + (int64_t)h * sl.s_wr);
+  float* w = sl.w;
+  const int64_t s_wr = sl.s_wr;
+  select_head<D, kT, kMaxG>(S.u.sel, H, st.C, n_act, end, G, sl.budget, sl.group, sl.scale,
+                            [&](int r, int c, float x) { w[(int64_t)(per_head ? h * G + r : h) * s_wr + c] = x; });
 }
 
+template <int D>
 __global__ __launch_bounds__(kT) void index_kernel(IndexArgs A) {
   __shared__ IndexSmem S;
   const int h = blockIdx.x;
   int end = 0;
   if (A.do_insert) {
-    insert_phase(S, A, h);
+    insert_phase<D>(S, A, h);
     end = S.scali[2];
   } else {
     end = A.st.end[h];
   }
-  if (A.do_select) select_phase(S, A, h, end);
+  if (A.do_select) select_phase<D>(S, A, h, end);
 }
 
 // ---- prefill ---------------------------------------------------------------------------------
@@ -551,13 +430,23 @@ __device__ __forceinline__ const char* head_keys(const BuildArgs& A, int h) {
 }
 
 // Centre: ksum = ordered sum of the range's keys, mu = given or ksum / nb; reset the summaries.
+template <typename T>
 __global__ __launch_bounds__(kT) void center_kernel(BuildArgs A) {
   const int s = blockIdx.x, h = A.b.heads[s], tid = threadIdx.x;
   const int d = A.st.d, C = A.st.C, nb = A.nb;
-  Keys K{head_keys(A, h), A.b.k_dtype, A.b.s_kn};
+  KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
   if (tid < d) {
+    // left-to-right sum; loads are issued 32 positions ahead of the adds
     float ks = 0.f;
-    for (int p = A.b.start; p < A.b.end; ++p) ks = ks + K(p, tid);
+    int p = A.b.start;
+    for (; p + 32 <= A.b.end; p += 32) {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) v[u] = K(p + u, tid);
+#pragma unroll
+      for (int u = 0; u < 32; ++u) ks = ks + v[u];
+    }
+    for (; p < A.b.end; ++p) ks = ks + K(p, tid);
     A.st.ksum[(int64_t)h * d + tid] = ks;
     float mu;
     if (A.b.mu) mu = A.b.mu[(int64_t)s * d + tid];
@@ -581,19 +470,24 @@ __global__ __launch_bounds__(kT) void center_kernel(BuildArgs A) {
 }
 
 // Unit centred directions of the range's keys, their lengths and squared lengths.
+template <typename T, int D>
 __global__ __launch_bounds__(kT) void normalize_kernel(BuildArgs A) {
   const int s = blockIdx.y, h = A.b.heads[s];
-  const int j = blockIdx.x * kT + threadIdx.x, d = A.st.d;
+  const int j = blockIdx.x * kT + threadIdx.x;
   if (j >= A.nb) return;
-  Keys K{head_keys(A, h), A.b.k_dtype, A.b.s_kn};
-  const float* mu = A.st.mu_ref + (int64_t)h * d;
+  KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
+  const float* mu = A.st.mu_ref + (int64_t)h * D;
   const int p = A.b.start + j;
-  auto kr = [&](int i) { return K(p, i) - mu[i]; };
-  const float sq = cdot(kr, kr, d);
+  float kr[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) kr[i] = K(p, i) - mu[i];
+  const float sq = cdot([&](int i) { return kr[i]; }, [&](int i) { return kr[i]; }, D);
   const float mag = sqrtf(sq);
   const float magc = fmaxf(mag, 1e-12f);
-  float* x = A.b.xn + ((int64_t)s * A.nb + j) * d;
-  for (int i = 0; i < d; ++i) x[i] = (K(p, i) - mu[i]) / magc;
+  float4* x = reinterpret_cast<float4*>(A.b.xn + ((int64_t)s * A.nb + j) * D);
+#pragma unroll
+  for (int k = 0; k < D / 4; ++k)
+    x[k] = make_float4(kr[4 * k] / magc, kr[4 * k + 1] / magc, kr[4 * k + 2] / magc, kr[4 * k + 3] / magc);
   A.b.mag[(int64_t)s * A.nb + j] = mag;
   A.b.sq[(int64_t)s * A.nb + j] = sq;
 }
@@ -604,7 +498,15 @@ __global__ void rbar_kernel(BuildArgs A) {
   if (threadIdx.x != 0) return;
   float t = 0.f;
   const float* sq = A.b.sq + (int64_t)s * A.nb;
-  for (int j = 0; j < A.nb; ++j) t = t + sq[j];
+  int j = 0;
+  for (; j + 32 <= A.nb; j += 32) {
+    float v[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) v[u] = sq[j + u];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) t = t + v[u];
+  }
+  for (; j < A.nb; ++j) t = t + sq[j];
   A.st.rbar[h] = A.nb > 0 ? sqrtf(t / (float)A.nb) : 0.f;
 }
 
@@ -760,6 +662,19 @@ bool state_ok(const ssa_index_state_t* st) {
          st->d <= kMaxD && st->d % 8 == 0 && st->heads_per_layer > 0 && st->capacity > 0;
 }
 
+int launch_index(const IndexArgs& A, hipStream_t s) {
+  const dim3 g(A.st.n_heads), b(kT);
+  switch (A.st.d) {
+    case 16: hipLaunchKernelGGL(index_kernel<16>, g, b, 0, s, A); break;
+    case 32: hipLaunchKernelGGL(index_kernel<32>, g, b, 0, s, A); break;
+    case 64: hipLaunchKernelGGL(index_kernel<64>, g, b, 0, s, A); break;
+    case 128: hipLaunchKernelGGL(index_kernel<128>, g, b, 0, s, A); break;
+    case 256: hipLaunchKernelGGL(index_kernel<256>, g, b, 0, s, A); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" int ssa_insert(const ssa_index_state_t* st, const ssa_insert_args_t* ins, void* stream) {
@@ -769,8 +684,7 @@ extern "C" int ssa_insert(const ssa_index_state_t* st, const ssa_insert_args_t* 
   A.ins = *ins;
   A.do_insert = 1;
   A.do_select = 0;
-  hipLaunchKernelGGL(index_kernel, dim3(st->n_heads), dim3(kT), 0, reinterpret_cast<hipStream_t>(stream), A);
-  return hipGetLastError();
+  return launch_index(A, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const ssa_select_args_t* sel,
@@ -783,8 +697,7 @@ extern "C" int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* 
   A.sel = *sel;
   A.do_insert = ins ? 1 : 0;
   A.do_select = 1;
-  hipLaunchKernelGGL(index_kernel, dim3(st->n_heads), dim3(kT), 0, reinterpret_cast<hipStream_t>(stream), A);
-  return hipGetLastError();
+  return launch_index(A, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b, void* stream) {
@@ -798,10 +711,26 @@ extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b,
   A.nb = b->end - b->start;
   A.nblk = (A.nb + kKB - 1) / kKB;
   A.cap_value = 0.f;
-  hipLaunchKernelGGL(center_kernel, dim3(b->n_sel), dim3(kT), 0, s, A);
+  switch (b->k_dtype) {
+    case kBF16: hipLaunchKernelGGL(center_kernel<__hip_bfloat16>, dim3(b->n_sel), dim3(kT), 0, s, A); break;
+    case kF16: hipLaunchKernelGGL(center_kernel<__half>, dim3(b->n_sel), dim3(kT), 0, s, A); break;
+    default: hipLaunchKernelGGL(center_kernel<float>, dim3(b->n_sel), dim3(kT), 0, s, A); break;
+  }
   if (A.nb > 0) {
     dim3 gk((A.nb + kT - 1) / kT, b->n_sel);
-    hipLaunchKernelGGL(normalize_kernel, gk, dim3(kT), 0, s, A);
+    auto normalize = [&](auto tag) {
+      using T = decltype(tag);
+      switch (st->d) {
+        case 16: hipLaunchKernelGGL((normalize_kernel<T, 16>), gk, dim3(kT), 0, s, A); break;
+        case 32: hipLaunchKernelGGL((normalize_kernel<T, 32>), gk, dim3(kT), 0, s, A); break;
+        case 64: hipLaunchKernelGGL((normalize_kernel<T, 64>), gk, dim3(kT), 0, s, A); break;
+        case 128: hipLaunchKernelGGL((normalize_kernel<T, 128>), gk, dim3(kT), 0, s, A); break;
+        case 256: hipLaunchKernelGGL((normalize_kernel<T, 256>), gk, dim3(kT), 0, s, A); break;
+      }
+    };
+    if (b->k_dtype == kBF16) normalize(__hip_bfloat16{});
+    else if (b->k_dtype == kF16) normalize(__half{});
+    else normalize(0.f);
     hipLaunchKernelGGL(rbar_kernel, dim3(b->n_sel), dim3(64), 0, s, A);
     auto assign = [&](int write_labels) {
       switch (st->d) {

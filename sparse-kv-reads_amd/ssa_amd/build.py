@@ -1,8 +1,9 @@
 """Build libssa_hip.so (the HIP kernels and their C ABI) for gfx950, in the package directory.
 
-``attention.hip`` is compiled with the default FMA contraction; ``index.hip``, whose results
-must be reproducible bit for bit, with ``-ffp-contract=off``. Both are linked into one shared
-library next to this file, which ``ssa_amd._lib`` loads.
+Both sources are compiled with ``-ffp-contract=off``: the selection and insertion decisions
+(select.h, shared by both files) must be reproducible bit for bit, and the attention loops
+spell out their fused multiply-adds. Both are linked into one shared library next to this
+file, which ``ssa_amd._lib`` loads.
 """
 
 from __future__ import annotations
@@ -22,7 +23,7 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
           # packed fp32 instructions are kept out of every kernel
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-fhip-fp32-correctly-rounded-divide-sqrt", f"-I{INCLUDE}"]
-SOURCES = {"attention.hip": [], "index.hip": ["-ffp-contract=off"]}
+SOURCES = {"attention.hip": ["-ffp-contract=off"], "index.hip": ["-ffp-contract=off"]}
 
 
 def _hipcc() -> str:

@@ -32,7 +32,7 @@ class DenseAttentionGraph:
     def __init__(self, *, H: int, H_kv: int, d: int, dtype, device, block_n: int = 32, num_splits: int | None = None):
         self.G = H // H_kv
         self.d = d
-        S = num_splits or default_splits(device, H_kv)
+        S = num_splits or default_splits(device, H_kv, dense=True)
         self.work = SplitWork(H_kv, S, self.G, d, device)
         self.out = torch.empty(H, d, device=device, dtype=dtype)
 
@@ -75,14 +75,15 @@ class SphereIndexGraph(SphereIndexFused):
     def step(self, q, K, V, n_dev, insert: bool = True):
         """One decode step; ``K, V [H_kv, capacity, d]`` with position ``n - 1`` already written.
         ``insert=False`` when the keys leaving the window were already inserted for every layer
-        by one launch (``AllLayerInsert``)."""
-        sel = self._select_args(q, self.wbuf, self.budget, "sum_share")
-        sel.need_out = self.need_dev.data_ptr()
-        ins = self._insert_args(K, n_dev=n_dev) if insert else None
+        by one launch (``AllLayerInsert``). Launches: ``ssa_insert`` (unless ``insert=False``) and
+        ``ssa_sparse_step`` (selection and attention); ``wbuf`` receives the selection."""
         s = stream_ptr(q.device)
-        check(lib().ssa_select(self._state(), ins, sel, s), "ssa_select")
+        st = self._state()
+        if insert:
+            check(lib().ssa_insert(st, self._insert_args(K, n_dev=n_dev), s), "ssa_insert")
+        sel = self._select_args(q, self.wbuf, self.budget, "sum_share")
         a = attn_args(q, K, V, self.out, self.work, labels=self.labels, w=self.wbuf, n_dev=n_dev)
-        check(lib().ssa_label_attention(a, s), "ssa_label_attention")
+        check(lib().ssa_sparse_step(st, sel, a, s), "ssa_sparse_step")
         return self.out
 
     def _host_end(self) -> None:

@@ -31,10 +31,13 @@ def cu_count(device) -> int:
     return _CUS[key]
 
 
-def default_splits(device, n_heads: int) -> int:
-    """Split-K factor: about four workgroups per compute unit over all heads (the reference's
-    ``cdiv(4 * SMs, H_kv)``, src/ssa/kernels/labeled_attn.py:266)."""
-    return max(1, -(-4 * cu_count(device) // n_heads))
+def default_splits(device, n_heads: int, *, dense: bool = False) -> int:
+    """Split-K factor per head. The reference uses ``cdiv(4 * SMs, H_kv)``
+    (src/ssa/kernels/labeled_attn.py:266). Here: about two workgroups per compute unit for the
+    sparse kernels, at most 64 splits (so the fused merge issues all its loads at once), and four
+    per compute unit for the dense kernel, at most 256."""
+    per_cu, cap = (4, 256) if dense else (2, 64)
+    return max(1, min(cap, -(-per_cu * cu_count(device) // n_heads)))
 
 
 class SplitWork:
@@ -78,7 +81,11 @@ def _check_qkv(q, K, V):
 
 
 def attn_args(q, K, V, out, work: SplitWork, *, labels=None, w=None, n_dev=None, n_host=0, per_head=False):
-    """Fill the C-ABI argument block of one attention launch."""
+    """Fill the C-ABI argument block of one attention launch. Rows of q, K and V are read with
+    16-byte loads, so their base pointers and row strides must be 16-byte aligned."""
+    for name, t in (("q", q), ("K", K), ("V", V)):
+        if t.data_ptr() % 16 or any((st * t.element_size()) % 16 for st in t.stride()[:-1]):
+            raise AssertionError(f"{name} rows must be 16-byte aligned (base and row strides)")
     a = AttnArgs()
     a.q, a.s_qh, a.q_dtype = q.data_ptr(), q.stride(0), dtype_tag(q.dtype)
     a.k, a.s_kh, a.s_kn = K.data_ptr(), K.stride(0), K.stride(1)
@@ -121,7 +128,7 @@ def label_weighted_attention_compact(q: torch.Tensor, K: torch.Tensor, V: torch.
     w = w.to(torch.float32).contiguous()
     q = q.contiguous()
     S = num_splits or default_splits(q.device, H_kv)
-    S = max(1, min(S, -(-max(n, 1) // 64)))
+    S = max(1, min(S, 256, -(-max(n, 1) // 64)))
     work = _work(H_kv, S, G, d, q.device)
     if out is None:
         out = torch.empty(H, d, device=q.device, dtype=q.dtype)
@@ -146,7 +153,7 @@ def dense_attention(q, K, V, *, n: int | None = None, n_dev: torch.Tensor | None
     G = H // H_kv
     n = nk if n is None else n
     if work is None:
-        S = num_splits or default_splits(q.device, H_kv)
+        S = num_splits or default_splits(q.device, H_kv, dense=True)
         work = _work(H_kv, S, G, d, q.device)
     if out is None:
         out = torch.empty(H, d, device=q.device, dtype=q.dtype)

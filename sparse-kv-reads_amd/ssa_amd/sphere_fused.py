@@ -30,7 +30,7 @@ import torch
 
 from ._lib import (BuildArgs, IndexState, InsertArgs, SelectArgs, check, dtype_tag, lib, ptr, require_cuda,
                    stream_ptr)
-from .labeled_attn import label_weighted_attention_compact
+from .labeled_attn import _work, attn_args, default_splits
 
 GROUPS = ("per_head", "max", "max_rel", "sum_share")
 _GROUP_ID = {"sum_share": 0, "per_head": 1, "max": 2, "max_rel": 3}
@@ -368,14 +368,28 @@ class SphereIndexFused:
               "ssa_select")
         return self.labels[:, :n], w
 
-    def attend(self, q, K, V, *, n, budget, group="sum_share"):
-        """One decode step for this layer: update the clusters, select, and attend over the
-        selected rows. ``K, V [H_kv, >= n, d]`` (engine cache layout, read in place).
-        Returns ``(out, labels, w)``."""
+    def attend(self, q, K, V, *, n, budget, group="sum_share", num_splits: int | None = None):
+        """One decode step for this layer: update the clusters (``ssa_insert``), then select and
+        attend over the selected rows in one launch (``ssa_sparse_step``). ``K, V [H_kv, >= n, d]``
+        (engine cache layout, read in place). Returns ``(out, labels, w)``."""
+        if group not in GROUPS:
+            raise ValueError(f"unknown group mode {group!r}")
         self.observe(K, n)
-        labels, w = self.labels_and_weights(q, n=n, budget=budget, group=group)
-        out = label_weighted_attention_compact(q, K[:, :n], V[:, :n], labels, w)
-        return out, labels, w
+        H, d = q.shape
+        if H % self.H_kv != 0 or H // self.H_kv > 8 or d != self.d:
+            raise ValueError(f"q [{H}, {d}] does not fit {self.H_kv} KV heads of dim {self.d}")
+        if V.shape != K.shape or K.dtype != V.dtype:
+            raise AssertionError("K and V must share shape and dtype")
+        rows = H if group == "per_head" else self.H_kv
+        w = self._wbuf(group, rows)
+        q = q.contiguous()
+        S = max(1, min(num_splits or default_splits(q.device, self.H_kv), 64, -(-max(n, 1) // 64)))
+        work = _work(self.H_kv, S, H // self.H_kv, d, q.device)
+        out = torch.empty(H, d, device=q.device, dtype=q.dtype)
+        a = attn_args(q, K, V, out, work, labels=self.labels, w=w, n_host=n, per_head=group == "per_head")
+        check(lib().ssa_sparse_step(self._state(), self._select_args(q, w, budget, group), a, stream_ptr(q.device)),
+              "ssa_sparse_step")
+        return out, self.labels[:, :n], w
 
     # -- counters ------------------------------------------------------------------------------
     @property
