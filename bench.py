@@ -6,19 +6,20 @@ KV cache, context 32768, keys from the synthetic mixture-of-directions distribut
 20 / 40 %, each against the same GPU's dense split-K decode over the full cache.
 
 A step is what the reference's graph decoder runs per layer and token
-(src/ssa/kernels/graph_kernels.py:220-244): insertion of the key leaving the recent window,
-cluster scoring and selection (one kernel, ssa_select), then split-K attention over the
-selected rows with the log-sum-exp merge (one kernel, ssa_label_attention); both are captured
-in a hipGraph. Timing follows the reference's harness (src/ssa/harness/kernel_bench.py:34-49,
-165-214) with two changes for MI355X: events bracket each replay with work queued ahead (no
-host gap inside a measurement), and replays rotate over ROT independent caches (ROT x 134 MB,
-well above the 256 MB Infinity Cache) so every step reads its K/V rows from HBM.
+(src/ssa/kernels/graph_kernels.py:220-244): insertion of the key leaving the recent window (one
+kernel, ssa_insert), then cluster scoring, selection, label scan, split-K attention over the
+selected rows and the log-sum-exp merge (one kernel, ssa_sparse_step); both are captured in a
+hipGraph. Timing follows the reference's harness (src/ssa/harness/kernel_bench.py:34-49,
+165-214) with two changes for MI355X: one graph holds ROT steps, one per independent cache
+(ROT x 134 MB, well above the 256 MB Infinity Cache, so every step reads its K/V rows from HBM),
+and events bracket each replay of that graph with replays queued back to back, so the host's
+launch gaps never enter a measurement; per-step time is the replay time divided by ROT.
 
 Bytes per step follow the reference's accounting (src/ssa/attn/accounting.py:19-32) per
 (sequence, KV head): selected K+V rows 2*rows*d*2, label scan 2n, 6 B per row read, summaries
 C*(d+12) and centroids C*d (8-bit), inserted key 2d and its cluster's fp32 sum 8d. The roofline
-entry is the attention kernel alone: its algorithmic bytes (K+V rows + labels) over its own
-event-timed duration.
+entry is the fused selection + attention kernel alone: the bytes it must read (K+V rows, label
+scan, the int8 summaries it scores) over its own graph-timed duration per launch.
 
 The CPU baseline times the oracle's numpy restatement of the reference's CPU path
 (SphereIndexRef: observe one key, labels_and_weights, label_weighted_attention) at the same
@@ -72,7 +73,7 @@ class Set:
     """One independent (cache, index) pair; its length lives in ``n_dev`` (a slice of one
     tensor shared by all sets, so one launch advances every set)."""
 
-    def __init__(self, seed, n, extra, splits, device, n_dev):
+    def __init__(self, seed, n, extra, splits, device, n_dev, dense_splits=None):
         import torch
         from ssa_amd.graph_kernels import DenseAttentionGraph, SphereIndexGraph
         from ssa_amd.synth import make_cache
@@ -88,7 +89,7 @@ class Set:
         torch.cuda.synchronize()
         self.prefill_s = time.time() - t
         self.dense = DenseAttentionGraph(H=H, H_kv=H_KV, d=D, dtype=torch.bfloat16, device=device,
-                                         num_splits=splits)
+                                         num_splits=dense_splits)
 
 
 def capture(fns):
@@ -180,8 +181,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--rot", type=int, default=16, help="independent caches; one graph steps through all of them")
-    ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: four workgroups per CU)")
+    ap.add_argument("--splits", type=int, default=0, help="split-K factor of the sparse step (0: the default)")
+    ap.add_argument("--dense-splits", type=int, default=0, help="split-K factor of the dense baseline (0: default)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--budgets", type=str, default="", help="comma list of budgets to time (default: all)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only copy 256 MiB device-to-device 5 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -192,12 +197,25 @@ def main() -> int:
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calib_copy:
+        x = torch.ones(256 * 1024 * 1024 // 4, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": x.numel() * 4, "copies": 5}))
+        return 0
+    global BUDGETS
+    if args.budgets:
+        BUDGETS = tuple(float(b) for b in args.budgets.split(","))
+        if HEADLINE not in BUDGETS:
+            BUDGETS = BUDGETS + (HEADLINE,)
     splits = args.splits or None
     reps = max(args.steps // args.rot, 4)
     extra = (args.warmup + 3) * len(BUDGETS) + reps * (len(BUDGETS) + 1) + 64
     n_all = torch.full((args.rot,), N, dtype=torch.int32, device=dev)
     log(f"building {args.rot} caches of {N} tokens ...")
-    sets = [Set(s, N, extra, splits, dev, n_all[s:s + 1]) for s in range(args.rot)]
+    sets = [Set(s, N, extra, splits, dev, n_all[s:s + 1], args.dense_splits or None) for s in range(args.rot)]
     log(f"prefill (k-means fit, binning, summaries) per cache: {sets[0].prefill_s:.3f} s (first), "
         f"{sets[-1].prefill_s:.3f} s (last)")
     advance = lambda: n_all.add_(1)                                   # noqa: E731
@@ -261,13 +279,14 @@ def main() -> int:
         "config": {"workload": "configs[1]: one layer, B=1, 16 q / 8 kv heads, d=128, bf16 cache, ctx 32768, "
                                "256 k-means clusters, window 64", "batch": 1, "context": N, "heads": [H, H_KV],
                    "head_dim": D, "clusters": C, "budgets": list(BUDGETS), "rotation_caches": args.rot,
-                   "splits": sets[0].idx.work.S, "context_at_end": n_now},
+                   "splits": sets[0].idx.work.S, "dense_splits": sets[0].dense.work.S, "context_at_end": n_now},
         "detail": {**detail, "insert_us": round(res["insert"][0], 2), "dense_us": round(dense_us, 2),
                    "dense_GBs": round(2 * H_KV * N * D * 2 / dense_us / 1e3, 1),
                    "prefill_s": round(sets[-1].prefill_s, 4)},
         "roofline": {"bound": "hbm", "kernel": "ssa_sparse_step (decode_kernel, fused selection)",
                      "achieved": round(achieved, 1),
-                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
+                     "traffic": _profiled_traffic(),
                      "bytes_per_launch": attn_bytes(rows20, N), "avg_launch_us": round(attn_mean, 3)},
     }
     if not args.no_cpu:
@@ -275,6 +294,19 @@ def main() -> int:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def _profiled_traffic():
+    """HBM bytes per launch of the fused kernel at the headline workload, as measured by
+    rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated) and recorded in profiles/."""
+    p = ROOT / "profiles" / "sparse_step_32k_b1_traffic.md"
+    try:
+        for line in p.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def _fused_only(st):

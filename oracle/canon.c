@@ -22,7 +22,7 @@
  *              Taylor in Horner form with fma, times 2^k; 0 below -87
  *   sums       left to right from +0; softmax denominators as a pairwise tree over the C slots;
  *              prefill sums in blocks of 256 keys (each block left to right), then over blocks
- * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, so only the explicit fmaf are fused).
+ * Build: oracle/Makefile (gcc -O3 -mfma -ffp-contract=off, so only the explicit fmaf are fused).
  */
 #include <math.h>
 #include <stdint.h>

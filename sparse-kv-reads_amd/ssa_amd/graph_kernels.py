@@ -7,10 +7,11 @@ inside the selection kernel.
 
 Mirrors src/ssa/kernels/graph_kernels.py:
   * ``DenseAttentionGraph`` (:171-189): exact split-K decode over ``[0, n)``, one launch.
-  * ``SphereIndexGraph`` (:192-279): per step two launches, ``ssa_select`` (insertion of the key
-    that left the window, scoring, selection) and ``ssa_label_attention`` (selection scan,
-    split-K attention over the selected rows, log-sum-exp merge), where the reference issues
-    bin, score, pick, zero, compact, list and merge.
+  * ``SphereIndexGraph`` (:192-279): per step two launches, ``ssa_insert`` (binning of the key
+    that left the window, in-kernel split of an over-cap cluster) and ``ssa_sparse_step`` (each
+    workgroup scores the clusters and takes the selection in LDS, scans the labels, runs
+    split-K attention over the selected rows, and the last workgroup of a head merges the
+    splits), where the reference issues bin, score, pick, zero, compact, list and merge.
   * ``AllLayerInsert`` (:286-325): one insertion launch for every layer.
 """
 

@@ -33,11 +33,10 @@ def cu_count(device) -> int:
 
 def default_splits(device, n_heads: int, *, dense: bool = False) -> int:
     """Split-K factor per head. The reference uses ``cdiv(4 * SMs, H_kv)``
-    (src/ssa/kernels/labeled_attn.py:266). Here: about two workgroups per compute unit for the
-    sparse kernels, at most 64 splits (so the fused merge issues all its loads at once), and four
-    per compute unit for the dense kernel, at most 256."""
-    per_cu, cap = (4, 256) if dense else (2, 64)
-    return max(1, min(cap, -(-per_cu * cu_count(device) // n_heads)))
+    (src/ssa/kernels/labeled_attn.py:266). Here: one workgroup per compute unit over all heads, at
+    most 32 splits per head, for both the sparse and the dense kernels: the last workgroup of a
+    head then issues every load of its merge at once (measured best on MI355X at 32k context)."""
+    return max(1, min(32, -(-cu_count(device) // n_heads)))
 
 
 class SplitWork:

@@ -10,7 +10,7 @@ keys join their nearest centroid, and a cluster that passes its size cap is spli
 the insertion kernel.
 
 All arithmetic runs in libssa_hip.so (insertion ``ssa_insert``, selection ``ssa_select``, prefill
-``ssa_build``, attention ``ssa_label_attention``); the host only allocates state, keeps the
+``ssa_build``, selection + attention ``ssa_sparse_step``); the host only allocates state, keeps the
 counters the reference keeps, and reads the drift flags every ``check_every`` steps (without a
 synchronisation when ``async_check``).
 
@@ -383,7 +383,7 @@ class SphereIndexFused:
         rows = H if group == "per_head" else self.H_kv
         w = self._wbuf(group, rows)
         q = q.contiguous()
-        S = max(1, min(num_splits or default_splits(q.device, self.H_kv), 64, -(-max(n, 1) // 64)))
+        S = max(1, min(num_splits or default_splits(q.device, self.H_kv), 256, -(-max(n, 1) // 64)))
         work = _work(self.H_kv, S, H // self.H_kv, d, q.device)
         out = torch.empty(H, d, device=q.device, dtype=q.dtype)
         a = attn_args(q, K, V, out, work, labels=self.labels, w=w, n_host=n, per_head=group == "per_head")
