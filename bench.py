@@ -6,10 +6,12 @@ KV cache, context 32768, keys from the synthetic mixture-of-directions distribut
 20 / 40 %, each against the same GPU's dense split-K decode over the full cache.
 
 A step is what the reference's graph decoder runs per layer and token
-(src/ssa/kernels/graph_kernels.py:220-244): insertion of the key leaving the recent window (one
-kernel, ssa_insert), then cluster scoring, selection, label scan, split-K attention over the
-selected rows and the log-sum-exp merge (one kernel, ssa_sparse_step); both are captured in a
-hipGraph. Timing follows the reference's harness (src/ssa/harness/kernel_bench.py:34-49,
+(src/ssa/kernels/graph_kernels.py:220-244): insertion of the key leaving the recent window,
+cluster scoring, selection, label scan, split-K attention over the selected rows and the
+log-sum-exp merge. Here that is one kernel, ssa_sparse_step, captured in a hipGraph: it selects
+and attends on the state binned for the current length, and its last workgroup per head then
+bins the key that leaves the window at the next length (the reference bins it at the start of
+the next step; the state each selection sees is the same). Timing follows the reference's harness (src/ssa/harness/kernel_bench.py:34-49,
 165-214) with two changes for MI355X: one graph holds ROT steps, one per independent cache
 (ROT x 134 MB, well above the 256 MB Infinity Cache, so every step reads its K/V rows from HBM),
 and events bracket each replay of that graph with replays queued back to back, so the host's
@@ -188,6 +190,8 @@ def main() -> int:
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy 256 MiB device-to-device 5 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2),
+                    help="1: the headline workload; 2: the batched sweep of configs[2] (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the clustered sparse decode step of one "
@@ -205,6 +209,15 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"calib_copy_bytes": x.numel() * 4, "copies": 5}))
         return 0
+    if args.config == 2:
+        res = batched_sweep(args, dev)
+        print(json.dumps({"metric": "configs[2] batched sparse decode-attention sweep (us, GB/s)", "unit": "us",
+                          "n_gpus": 1, "dtype": "bf16", "data": "synthetic (ssa_amd.synth)", "peak_GBs": PEAK_GBS,
+                          "config": {"workload": "configs[2]: B x ctx in " + str(list(BATCHED)) + ", 16 q / 8 kv "
+                                     "heads per sequence, d=128, bf16, 256 k-means clusters, window 64",
+                                     "budgets": list(BATCHED_BUDGETS)},
+                          "results": res}), flush=True)
+        return 0
     global BUDGETS
     if args.budgets:
         BUDGETS = tuple(float(b) for b in args.budgets.split(","))
@@ -221,7 +234,6 @@ def main() -> int:
     advance = lambda: n_all.add_(1)                                   # noqa: E731
 
     graphs = {"dense": capture([lambda st=st: st.dense(st.q, st.K, st.V, st.n_dev) for st in sets])}
-    graphs["insert"] = capture([lambda st=st: _insert_only(st) for st in sets])
     for b in BUDGETS:
         for st in sets:
             st.idx.budget = b
@@ -237,7 +249,6 @@ def main() -> int:
         res[("step", b)] = time_graph(graphs[("step", b)], reps, R, advance=advance)
         res[("attn", b)] = time_graph(graphs[("attn", b)], reps, R)
         res[("rows", b)] = sets[-1].idx.work.cnt.tolist()      # rows read per head, counted by the kernel
-    res["insert"] = time_graph(graphs["insert"], reps, R, advance=advance)
     time_graph(graphs["dense"], 3, R)
     res["dense"] = time_graph(graphs["dense"], reps, R)
 
@@ -280,7 +291,8 @@ def main() -> int:
                                "256 k-means clusters, window 64", "batch": 1, "context": N, "heads": [H, H_KV],
                    "head_dim": D, "clusters": C, "budgets": list(BUDGETS), "rotation_caches": args.rot,
                    "splits": sets[0].idx.work.S, "dense_splits": sets[0].dense.work.S, "context_at_end": n_now},
-        "detail": {**detail, "insert_us": round(res["insert"][0], 2), "dense_us": round(dense_us, 2),
+        "detail": {**detail, "insert_ahead_us": round(res[("step", HEADLINE)][0] - res[("attn", HEADLINE)][0], 2),
+                   "dense_us": round(dense_us, 2),
                    "dense_GBs": round(2 * H_KV * N * D * 2 / dense_us / 1e3, 1),
                    "prefill_s": round(sets[-1].prefill_s, 4)},
         "roofline": {"bound": "hbm", "kernel": "ssa_sparse_step (decode_kernel, fused selection)",
@@ -294,6 +306,77 @@ def main() -> int:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
+
+
+BATCHED = ((8, 8192), (2, 32768), (16, 32768), (64, 32768))
+BATCHED_BUDGETS = (0.20, 0.05)
+
+
+def batched_sweep(args, dev) -> dict:
+    """batch x context in BATCHED, budgets 20% / 5%, every sequence with its own
+    seeded clusters (batch folded into the KV heads). Per shape: the whole step (insert + fused
+    selection and attention), the fused kernel alone and the dense baseline, each as a graph of
+    ``rot`` steps over independent caches (at least 1 GB of K/V per graph, so rows come from HBM)."""
+    import torch
+    from ssa_amd.graph_kernels import DenseAttentionGraph, SphereIndexGraph
+    from ssa_amd.synth import make_cache
+    out = {}
+    for B, n in BATCHED:
+        hk = B * H_KV
+        kv_bytes = 2 * hk * n * D * 2
+        rot = max(1, -(-(1 << 30) // kv_bytes))
+        reps = max(args.steps // rot, 4) if rot > 1 else max(args.steps // 8, 4)
+        extra = (args.warmup + 3) * len(BATCHED_BUDGETS) + reps * (len(BATCHED_BUDGETS) + 1) + 64
+        cap = n + extra
+        n_all = torch.full((rot,), n, dtype=torch.int32, device=dev)
+        sets = []
+        t0 = time.time()
+        for r in range(rot):
+            K, V, q, _ = make_cache(B, H_KV, cap, D, H=H, centers=C, capacity=cap, seed=100 + r,
+                                    dtype=torch.bfloat16, device=dev, gen_device=str(dev))
+            K, V, q = K.view(hk, cap, D), V.view(hk, cap, D), q.view(B * H, D)
+            idx = SphereIndexGraph(budget=BATCHED_BUDGETS[0], C=C, window=WINDOW, delta=0.03, capacity=cap,
+                                   check_every=10 ** 9, partition="kmeans")
+            idx.prepare(K, n, B * H)
+            dense = DenseAttentionGraph(H=B * H, H_kv=hk, d=D, dtype=torch.bfloat16, device=dev)
+            sets.append((K, V, q, idx, dense, n_all[r:r + 1]))
+        torch.cuda.synchronize()
+        log(f"B={B} n={n}: {rot} caches built in {time.time() - t0:.1f} s")
+        advance = lambda: n_all.add_(1)                               # noqa: E731
+        gd = capture([lambda s=s: s[4](s[2], s[0], s[1], s[5]) for s in sets])
+        time_graph(gd, 3, rot)
+        dense_us = time_graph(gd, reps, rot)[0]
+        row = {"rotation_caches": rot, "kv_heads": hk, "splits": sets[0][3].work.S, "dense_us": round(dense_us, 2),
+               "dense_GBs": round(kv_bytes / dense_us / 1e3, 1)}
+        for b in BATCHED_BUDGETS:
+            for s in sets:
+                s[3].budget = b
+            gs = capture([lambda s=s: s[3].step(s[2], s[0], s[1], s[5]) for s in sets])
+            ga = capture([lambda s=s: _fused_only(_Shim(*s)) for s in sets])
+            time_graph(gs, args.warmup, rot, advance=advance)
+            step_us = time_graph(gs, reps, rot, advance=advance)[0]
+            attn_us = time_graph(ga, reps, rot)[0]
+            rows = sets[-1][3].work.cnt.tolist()
+            by = attn_bytes(rows, n)
+            row[f"{int(b * 100)}%"] = {
+                "step_us": round(step_us, 2), "select_attention_us": round(attn_us, 2),
+                "rows_per_head": int(sum(rows) / len(rows)),
+                "attention_GBs": round(by / attn_us / 1e3, 1), "attention_frac": round(by / attn_us / 1e3 / PEAK_GBS, 4),
+                "step_effective_GBs": round(step_bytes(rows, n) / step_us / 1e3, 1),
+                "speedup_vs_dense": round(dense_us / step_us, 2)}
+            del gs, ga
+        out[f"{B}x{n}"] = row
+        log(json.dumps({f"{B}x{n}": row}))
+        del sets, gd
+        torch.cuda.empty_cache()
+    return out
+
+
+class _Shim:
+    """Adapter giving ``_fused_only`` the attributes of a ``Set``."""
+
+    def __init__(self, K, V, q, idx, dense, n_dev):
+        self.K, self.V, self.q, self.idx, self.n_dev = K, V, q, idx, n_dev
 
 
 def _profiled_traffic():
@@ -316,15 +399,7 @@ def _fused_only(st):
     idx = st.idx
     sel = idx._select_args(st.q, idx.wbuf, idx.budget, "sum_share")
     a = attn_args(st.q, st.K, st.V, idx.out, idx.work, labels=idx.labels, w=idx.wbuf, n_dev=st.n_dev)
-    check(lib().ssa_sparse_step(idx._state(), sel, a, stream_ptr(st.q.device)), "ssa_sparse_step")
-
-
-def _insert_only(st):
-    """The insertion launch of one step."""
-    from ssa_amd._lib import check, lib, stream_ptr
-    idx = st.idx
-    check(lib().ssa_insert(idx._state(), idx._insert_args(st.K, n_dev=st.n_dev), stream_ptr(st.q.device)),
-          "ssa_insert")
+    check(lib().ssa_sparse_step(idx._state(), sel, a, None, stream_ptr(st.q.device)), "ssa_sparse_step")
 
 
 if __name__ == "__main__":

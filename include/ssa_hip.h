@@ -132,10 +132,16 @@ int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const 
  * computes its head's selection exactly as ssa_select does (same bits, from the index state and
  * sel), then attends over the selected rows as ssa_label_attention does. args->labels must be
  * st->labels; sel->w, if non-NULL, receives the selection (written by one workgroup per head).
- * Replaces the per-layer score + pick + compact + list + merge launches of
+ * With ins_ahead non-NULL (one layer's state, ins_ahead->k the attention's K, no koff), once
+ * every workgroup of a head has read the state, the last one inserts the keys that leave the
+ * window at length n + 1 (ins_ahead's n fields are ignored), splits included: the state is then
+ * what ssa_insert would make of it at the start of the next step, so a decode loop that grows n
+ * by one per step needs no insertion launch. The keys at positions < n + 1 - window must be in
+ * the cache.
+ * Replaces the per-layer bin + score + pick + compact + list + merge launches of
  * SphereIndexGraph.step (src/ssa/kernels/graph_kernels.py:220-244). */
 int ssa_sparse_step(const ssa_index_state_t* st, const ssa_select_args_t* sel, const ssa_attn_args_t* args,
-                    void* stream);
+                    const ssa_insert_args_t* ins_ahead, void* stream);
 
 /* ---- prefill: fit, bin and summarise the prompt's keys ------------------------------------- */
 

@@ -1,0 +1,596 @@
+// Split-K decode attention over a KV cache read in place (gfx950).
+//
+//   out[h] = sum_j w[label_j] e^{s_j} v_j / sum_j w[label_j] e^{s_j},   s_j = q_h . k_j / sqrt(d)
+//
+// Reference behaviour: label_weighted_attention (src/ssa/attn/labeled.py:24-44), computed by the
+// reference GPU path as compact_positions + _list_kernel + merge_splits
+// (src/ssa/kernels/labeled_attn.py:166-278) and, for the dense baseline, _dense_dev_kernel
+// (src/ssa/kernels/graph_kernels.py:28-59).
+//
+// Design (one kernel per call, no index list in HBM):
+//   grid (S, Hk): workgroup (sp, h) owns positions [sp*chunk, (sp+1)*chunk) of KV head h.
+//   Labelled mode scans its positions' 2-byte labels, looks their weights up in an LDS copy
+//   of w, and compacts the selected positions into an LDS list (ballot + popcount), so only
+//   selected K/V rows are ever fetched. Dense mode walks its rows directly.
+//   Rows are read as 16-byte-per-lane loads: D/8 lanes cover one 128-dim bf16 row (256 B), so
+//   one wave instruction reads 64*16 B of consecutive row bytes; each lane group keeps its own
+//   online softmax (base-2, q pre-scaled by log2(e)/sqrt(d)) over the G query heads that share
+//   the KV head, and issues U rows of K and V before it consumes any of them.
+//   States merge across lane groups (DPP/shuffle), across waves (LDS), then across the S
+//   workgroups of a head: each writes its partial with agent-scope stores and counts itself in
+//   on an agent-scope atomic counter; the last workgroup to arrive (which resets the counter
+//   for the next launch) combines the partials by log-sum-exp and writes out[h*G + g] in the
+//   output dtype, plus the count of rows read.
+//   Fused mode (ssa_sparse_step) first computes the head's cluster selection in LDS
+//   (select.h) and uses it as the weights.
+#pragma once
+
+#include "insert.h"
+
+namespace ssa {
+
+struct DecodeParams {
+  const void* q; int64_t s_qh; int q_dtype;
+  const void* k; int64_t s_kh, s_kn;
+  const void* v; int64_t s_vh, s_vn;
+  const int16_t* labels; int64_t s_lh;
+  const float* w; int64_t s_wr; int w_len; int per_head;
+  const int32_t* n_dev; int n_host;
+  float* part_m; float* part_l; float* part_a; int32_t* part_cnt;
+  int32_t* counter;
+  void* out; int64_t s_oh; int out_dtype;
+  int32_t* cnt_out;
+  int n_heads, G, S;
+  float qscale;        // log2(e)/sqrt(d)
+  int chunk_align;
+  // fused selection (ssa_sparse_step): the index state and the selection parameters
+  ssa_index_state_t st;
+  double budget; int group; float sel_scale;
+  // insertion ahead (fused mode with AHEAD): after the merge, the last workgroup of each head
+  // bins the keys that leave the window at length n + 1
+  ssa_insert_args_t ins;
+};
+
+constexpr int kThreads = 256;
+static_assert(kThreads == kT, "the insertion code runs on the decode kernel's workgroup");
+constexpr int kWaves = kThreads / 64;
+constexpr int kPage = 1024;          // positions compacted per pass
+constexpr int kMaxW = 1025;          // weight slots (C + 1) held in LDS per row
+
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+  // Sum over the LPR consecutive lanes that hold one row (LPR a power of two, 2..32).
+  if constexpr (LPR >= 2) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+  if constexpr (LPR >= 4) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+  if constexpr (LPR >= 8) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, true));
+  if constexpr (LPR >= 16) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, true));
+  if constexpr (LPR >= 32) x += __shfl_xor(x, 16, 64);
+  return x;
+}
+
+constexpr int kRowsInFlight = 8;     // rows of K (and of V) each lane group loads before using them
+
+// 8 consecutive elements of a row in their storage type: 16 bytes for bf16/fp16, 32 for fp32.
+struct F8 { float4 a, b; };
+template <typename T> struct RawRow { using type = uint4; };
+template <> struct RawRow<float> { using type = F8; };
+
+__device__ __forceinline__ void widen8(const uint4& r, float (&f)[8], __hip_bfloat16*) {
+  const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(u[e] << 16);
+    f[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void widen8(const uint4& r, float (&f)[8], __half*) {
+  const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const __half2 h2 = *reinterpret_cast<const __half2*>(&u[e]);
+    f[2 * e] = __low2float(h2);
+    f[2 * e + 1] = __high2float(h2);
+  }
+}
+__device__ __forceinline__ void widen8(const F8& r, float (&f)[8], float*) {
+  f[0] = r.a.x; f[1] = r.a.y; f[2] = r.a.z; f[3] = r.a.w;
+  f[4] = r.b.x; f[5] = r.b.y; f[6] = r.b.z; f[7] = r.b.w;
+}
+
+__device__ __forceinline__ void store_out(void* out, int dt, int64_t i, float x) {
+  if (dt == kBF16) reinterpret_cast<__hip_bfloat16*>(out)[i] = __float2bfloat16(x);
+  else if (dt == kF16) reinterpret_cast<__half*>(out)[i] = __float2half(x);
+  else reinterpret_cast<float*>(out)[i] = x;
+}
+
+constexpr int kMaxS = 256;           // splits per head (host clamps)
+constexpr int kMergeBatch = 8;       // accumulator loads (float4) each merging thread issues at once
+
+// Agent-scope relaxed load: coherent with the agent-scope stores of other workgroups on any XCD.
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int GMAX, bool DENSE>
+struct DecodeSmem {
+  static constexpr int kSelG = DENSE ? 1 : GMAX;
+  float lw[DENSE ? 1 : GMAX][DENSE ? 1 : kMaxW];       // log2 w per weight row, -inf where w <= 0
+  union {
+    struct {
+      int pos[kPage];                                    // selected positions of the current page
+      float rlw[GMAX][kPage];                            // their log2 w per weight row
+    } list;
+    SelSmem<kSelG> sel;                                  // fused selection scratch
+    InsertSmem tail;                                     // fused insertion ahead
+    struct {
+      float f[kMaxS * GMAX];                             // rescale factor per (split, head)
+      float4 acc[kThreads];
+    } mrg;
+  } u;
+  int scan[kPage / kThreads][kWaves];                 // selected positions per (page slice, wave)
+  float red_m[kWaves][GMAX], red_l[kWaves][GMAX];
+  float red_a[kWaves][GMAX][D];
+  float gden[GMAX];
+  int red_i[kWaves];
+  int last;
+};
+
+// DENSE: every position in [0, n) is read with weight 1. Otherwise positions are selected by
+// w[label] > 0 (any query head of the group, when w has one row per query head). SELECT: w is
+// not read but computed by this workgroup from the index state (select.h), the same bits the
+// selection kernel writes; workgroup 0 of each head also stores it.
+template <typename T, int D, int GMAX, bool DENSE, bool SELECT = false, bool AHEAD = false>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
+  constexpr int LPR = D / 8;           // lanes per row
+  constexpr int RPI = 64 / LPR;        // rows per wave instruction
+  constexpr int U = kRowsInFlight;     // rows in flight per lane group
+  constexpr int PER = kPage / kThreads;
+  using Raw = typename RawRow<T>::type;
+  __shared__ DecodeSmem<D, GMAX, DENSE> sm;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane / LPR, li = lane % LPR;
+  const int sp = blockIdx.x, h = blockIdx.y;
+  const int G = a.G, S = a.S;
+  const bool per_head = !DENSE && a.per_head;
+
+  const int n = a.n_dev ? *a.n_dev : a.n_host;
+  int chunk = (n + S - 1) / S;
+  chunk = (chunk + a.chunk_align - 1) / a.chunk_align * a.chunk_align;
+  const int s0 = min(sp * chunk, n);
+  const int s1 = min(s0 + chunk, n);
+  const int16_t* labrow = DENSE ? nullptr : a.labels + (int64_t)h * a.s_lh;
+
+  // Issue the selection state's and the first page's label loads before anything waits on memory.
+  SelPre<D> pre;
+  if constexpr (SELECT) sel_prefetch<D>(pre, head_view(a.st, h), a.st.C);
+  int lbl[PER];
+  if constexpr (!DENSE) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int j = s0 + u * kThreads + tid;
+      lbl[u] = j < s1 ? (int)labrow[j] : 0;
+    }
+  }
+
+  // q rows of the group: one uniform dtype branch, then 16-byte loads (rows 16-byte aligned)
+  float qr[GMAX][8];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    const int64_t off = (int64_t)(h * G + min(g, G - 1)) * a.s_qh + li * 8;
+    float r[8];
+    if (a.q_dtype == kBF16) widen8(*reinterpret_cast<const uint4*>(reinterpret_cast<const __hip_bfloat16*>(a.q) + off), r, (__hip_bfloat16*)nullptr);
+    else if (a.q_dtype == kF16) widen8(*reinterpret_cast<const uint4*>(reinterpret_cast<const __half*>(a.q) + off), r, (__half*)nullptr);
+    else {
+      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.q) + off);
+      const float4 x = p[0], y = p[1];
+      r[0] = x.x; r[1] = x.y; r[2] = x.z; r[3] = x.w; r[4] = y.x; r[5] = y.y; r[6] = y.z; r[7] = y.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qr[g][e] = g < G ? r[e] * a.qscale : 0.f;
+    if constexpr (SELECT) {
+      // lane group 0 of wave 0 holds the whole row: the selection's fp32 copy (rows >= G zero)
+      if (wave == 0 && lg == 0) {
+        float4* dst = reinterpret_cast<float4*>(&sm.u.sel.q[g][li * 8]);
+        dst[0] = g < G ? make_float4(r[0], r[1], r[2], r[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        dst[1] = g < G ? make_float4(r[4], r[5], r[6], r[7]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+
+  if constexpr (SELECT) {
+    // the head's selection, computed here while the label loads are in flight
+    const int n_act = a.st.n_c[h], end = a.st.end[h];
+    __syncthreads();
+    float* wout = const_cast<float*>(a.w);
+    const int64_t s_wr = a.s_wr;
+    const bool store_w = sp == 0 && wout != nullptr;
+    select_head<D, kThreads, GMAX>(sm.u.sel, head_view(a.st, h), pre, a.st.C, n_act, end, G, a.budget, a.group,
+                                   a.sel_scale, [&](int r, int c, float x) {
+                                     sm.lw[r][c] = x > 0.f ? 0.f : -INFINITY;
+                                     if (store_w) wout[(int64_t)(per_head ? h * G + r : h) * s_wr + c] = x;
+                                   });
+  } else if constexpr (!DENSE) {
+    const int nrow = per_head ? G : 1;
+    for (int r = 0; r < nrow; ++r) {
+      const float* wr = a.w + (int64_t)(per_head ? h * G + r : h) * a.s_wr;
+      float x[(kMaxW + kThreads - 1) / kThreads];
+#pragma unroll
+      for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
+        const int c = tid + k * kThreads;
+        x[k] = c < a.w_len ? wr[c] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
+        const int c = tid + k * kThreads;
+        if (c < a.w_len) sm.lw[r][c] = x[k] > 0.f ? __log2f(x[k]) : -INFINITY;
+      }
+    }
+  }
+
+  float m_[GMAX], l_[GMAX], acc[GMAX][8];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    m_[g] = kNeg;
+    l_[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+
+  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)h * a.s_kh + li * 8;
+  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)h * a.s_vh + li * 8;
+  int rows_read = 0;
+
+  for (int p0 = s0; p0 < s1; p0 += kPage) {
+    const int pn = min(kPage, s1 - p0);
+    int R;
+    if constexpr (DENSE) {
+      R = pn;
+    } else {
+      if (p0 != s0) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const int j = p0 + u * kThreads + tid;
+          lbl[u] = j < s1 ? (int)labrow[j] : 0;
+        }
+      }
+      __syncthreads();   // lw ready / previous page's list consumed
+      // Position p0 + u * kThreads + tid: the list in (u, wave, lane) order is ascending.
+      bool sel[PER];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int j = u * kThreads + tid;
+        lbl[u] = min(max(lbl[u], 0), a.w_len - 1);     // a bad label never indexes outside lw
+        bool s = false;
+        if (j < pn) {
+          if (per_head) {
+            for (int g = 0; g < G; ++g) s |= sm.lw[g][lbl[u]] != -INFINITY;
+          } else {
+            s = sm.lw[0][lbl[u]] != -INFINITY;
+          }
+        }
+        sel[u] = s;
+      }
+      const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      unsigned long long bal[PER];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        bal[u] = __ballot(sel[u]);
+        if (lane == 0) sm.scan[u][wave] = __popcll(bal[u]);
+      }
+      __syncthreads();
+      int total = 0;
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        int wbase = 0, tot_u = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+          const int c2 = sm.scan[u][w2];
+          if (w2 < wave) wbase += c2;
+          tot_u += c2;
+        }
+        if (sel[u]) {
+          const int o = total + wbase + __popcll(bal[u] & below);
+          sm.u.list.pos[o] = p0 + u * kThreads + tid;
+          if (per_head) {
+            for (int g = 0; g < G; ++g) sm.u.list.rlw[g][o] = sm.lw[g][lbl[u]];
+          } else {
+            sm.u.list.rlw[0][o] = sm.lw[0][lbl[u]];
+          }
+        }
+        total += tot_u;
+      }
+      R = total;
+      __syncthreads();
+    }
+    rows_read += R;
+
+    // ---- attention over the R rows of this page: every lane group issues U rows of K and V,
+    // then consumes them; rows past R re-read the last row and are masked out.
+    for (int base = 0; base < R; base += kWaves * RPI * U) {
+      Raw kraw[U], vraw[U];
+      int rr[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        rr[u] = base + u * kWaves * RPI + wave * RPI + lg;
+        const int rc = min(rr[u], R - 1);
+        int pos;
+        if constexpr (DENSE) pos = p0 + rc;
+        else pos = sm.u.list.pos[rc];
+        kraw[u] = *reinterpret_cast<const Raw*>(kbase + (int64_t)pos * a.s_kn);
+        vraw[u] = *reinterpret_cast<const Raw*>(vbase + (int64_t)pos * a.s_vn);
+      }
+      float s[GMAX][U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float kf[8];
+        widen8(kraw[u], kf, (T*)nullptr);
+        float lw0 = 0.f;
+        if constexpr (!DENSE) lw0 = rr[u] < R ? sm.u.list.rlw[0][min(rr[u], R - 1)] : -INFINITY;
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kf[e], d);
+          d = row_sum<LPR>(d);
+          float lw = lw0;
+          if constexpr (!DENSE) {
+            if (per_head && g < G) lw = rr[u] < R ? sm.u.list.rlw[g][min(rr[u], R - 1)] : -INFINITY;
+          }
+          s[g][u] = rr[u] < R ? d + lw : -INFINITY;
+        }
+      }
+      float p[GMAX][U];
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) {
+        float mx = m_[g];
+#pragma unroll
+        for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[g][u]);
+        const float alpha = __builtin_amdgcn_exp2f(m_[g] - mx);
+        float psum = 0.f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) { p[g][u] = __builtin_amdgcn_exp2f(s[g][u] - mx); psum += p[g][u]; }
+        l_[g] = fmaf(l_[g], alpha, psum);
+        m_[g] = mx;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float vf[8];
+        widen8(vraw[u], vf, (T*)nullptr);
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p[g][u], vf[e], acc[g][e]);
+      }
+    }
+  }
+
+  // ---- merge the lane groups of each wave ---------------------------------------------------
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      const float m2 = __shfl_xor(m_[g], o, 64);
+      const float l2 = __shfl_xor(l_[g], o, 64);
+      const float M = fmaxf(m_[g], m2);
+      const float f1 = __builtin_amdgcn_exp2f(m_[g] - M), f2 = __builtin_amdgcn_exp2f(m2 - M);
+      l_[g] = l_[g] * f1 + l2 * f2;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a2 = __shfl_xor(acc[g][e], o, 64);
+        acc[g][e] = acc[g][e] * f1 + a2 * f2;
+      }
+      m_[g] = M;
+    }
+  }
+  if (lane < LPR) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      if (lane == 0) { sm.red_m[wave][g] = m_[g]; sm.red_l[wave][g] = l_[g]; }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.red_a[wave][g][li * 8 + e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the waves; publish this workgroup's partial -------------------------------------
+  // Partials are written with agent-scope stores (coherent across the XCDs' L2 caches), so the
+  // workgroup only has to wait for its own stores before it counts itself in: no L2 write-back.
+  const int64_t pidx = (int64_t)h * S + sp;
+  for (int t = tid; t < G * D; t += kThreads) {
+    const int g = t / D, dd = t % D;
+    float M = kNeg;
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, sm.red_m[w2][g]);
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves; ++w2) {
+      const float f = __builtin_amdgcn_exp2f(sm.red_m[w2][g] - M);
+      L = fmaf(sm.red_l[w2][g], f, L);
+      A = fmaf(sm.red_a[w2][g][dd], f, A);
+    }
+    __hip_atomic_store(a.part_a + (pidx * G + g) * D + dd, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (dd == 0) {
+      __hip_atomic_store(a.part_m + pidx * G + g, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.part_l + pidx * G + g, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(a.part_cnt + pidx, rows_read, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);       // this thread's stores have reached the coherence point
+  __syncthreads();
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(a.counter + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm.last = (old == S - 1);
+  }
+  __syncthreads();
+  if (!sm.last) return;
+  // the insertion ahead reads its state while the merge's loads are in flight
+  InsPre<AHEAD ? D : 16> ipre;
+  if constexpr (AHEAD) insert_prefetch<D>(ipre, a.st, a.ins, h, n + 1);
+  // ---- the last workgroup of head h merges the S partials ----------------------------------
+  // One round of loads, all issued before the first wait: this thread's accumulator columns
+  // (up to kMergeBatch splits) into registers and, in wave 0, every split's (max, sum) and row
+  // count spread over the lanes. The partials are read with agent-scope loads (coherent across
+  // XCDs), so no L2 invalidate is needed.
+  const int64_t hb = (int64_t)h * S;
+  const int cols4 = G * D / 4;
+  const float* pa = a.part_a + hb * G * D;
+  const int ncol0 = min(kThreads, cols4);
+  const int nsg0 = kThreads / ncol0;
+  const int sg0 = tid / ncol0, col0 = tid % ncol0;
+  // branchless: out-of-range splits re-read split S-1 and get weight 0 below
+  float4 va[kMergeBatch];
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) {
+    const int s2 = min(sg0 + k * nsg0, S - 1);
+    const float* src = pa + ((int64_t)s2 * cols4 + col0) * 4;
+    va[k].x = load_coherent(src + 0);
+    va[k].y = load_coherent(src + 1);
+    va[k].z = load_coherent(src + 2);
+    va[k].w = load_coherent(src + 3);
+  }
+  if (wave == 0) {
+    // lane l holds head g = l % GMAX of splits l / GMAX + (64 / GMAX) * i
+    constexpr int SPI = 64 / GMAX;                      // splits per round of lanes
+    constexpr int kML = (kMaxS + SPI - 1) / SPI;
+    const int g = lane % GMAX;
+    float mv[kML], lv[kML];
+    int cpart = 0;
+#pragma unroll
+    for (int i = 0; i < kML; ++i) {
+      if (i * SPI < S) {                                // uniform
+        const int s2 = lane / GMAX + SPI * i;
+        const int e = min(s2, S - 1) * G + min(g, G - 1);
+        const float m0 = load_coherent(a.part_m + hb * G + e);
+        const float l0 = load_coherent(a.part_l + hb * G + e);
+        const bool ok = s2 < S && g < G;
+        mv[i] = ok ? m0 : kNeg;
+        lv[i] = ok ? l0 : 0.f;
+      }
+    }
+    for (int t = lane; t < S; t += 64)
+      cpart += __hip_atomic_load(a.part_cnt + hb + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float M = kNeg;
+#pragma unroll
+    for (int i = 0; i < kML; ++i)
+      if (i * SPI < S) M = fmaxf(M, mv[i]);
+#pragma unroll
+    for (int o = GMAX; o < 64; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < kML; ++i) {
+      if (i * SPI < S) {
+        const int s2 = lane / GMAX + SPI * i;
+        const float f = __builtin_amdgcn_exp2f(mv[i] - M);
+        if (s2 < S && g < G) sm.u.mrg.f[s2 * G + g] = f;
+        den = fmaf(f, lv[i], den);
+      }
+    }
+#pragma unroll
+    for (int o = GMAX; o < 64; o <<= 1) den += __shfl_xor(den, o, 64);
+    if (lane < G) sm.gden[lane] = den;
+    cpart = wave_sum_i(cpart);
+    if (lane == 0) sm.red_i[0] = cpart;
+  }
+  __syncthreads();
+  // rescaled sum of the accumulators: float4 columns, splits strided over thread groups
+  for (int c0 = 0; c0 < cols4; c0 += kThreads) {
+    const int ncol = min(kThreads, cols4 - c0);
+    const int nsg = kThreads / ncol;
+    const int sg = tid / ncol, col = c0 + tid % ncol;
+    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (sg < nsg) {
+      const int g = col * 4 / D;
+      int s2 = sg;
+      if (c0 == 0) {                 // the batch already in registers
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+          const int sk = sg + k * nsg;
+          const float f = sk < S ? sm.u.mrg.f[min(sk, S - 1) * G + g] : 0.f;
+          acc4.x = fmaf(f, va[k].x, acc4.x); acc4.y = fmaf(f, va[k].y, acc4.y);
+          acc4.z = fmaf(f, va[k].z, acc4.z); acc4.w = fmaf(f, va[k].w, acc4.w);
+        }
+        s2 = sg + kMergeBatch * nsg;
+      }
+#pragma unroll 8
+      for (; s2 < S; s2 += nsg) {
+        const float f = sm.u.mrg.f[s2 * G + g];
+        const float* src = pa + ((int64_t)s2 * cols4 + col) * 4;
+        acc4.x = fmaf(f, load_coherent(src + 0), acc4.x); acc4.y = fmaf(f, load_coherent(src + 1), acc4.y);
+        acc4.z = fmaf(f, load_coherent(src + 2), acc4.z); acc4.w = fmaf(f, load_coherent(src + 3), acc4.w);
+      }
+    }
+    if (c0 > 0) __syncthreads();     // the previous chunk's sums have been read
+    sm.u.mrg.acc[tid] = acc4;
+    __syncthreads();
+    if (tid < ncol) {
+      float4 v = sm.u.mrg.acc[tid];
+      for (int s3 = 1; s3 < nsg; ++s3) {
+        const float4 w4 = sm.u.mrg.acc[s3 * ncol + tid];
+        v.x += w4.x; v.y += w4.y; v.z += w4.z; v.w += w4.w;
+      }
+      const int e0 = (c0 + tid) * 4, g = e0 / D, dd = e0 % D;
+      const float den = sm.gden[g];
+      const int64_t o = (int64_t)(h * G + g) * a.s_oh + dd;
+      store_out(a.out, a.out_dtype, o + 0, v.x / den);
+      store_out(a.out, a.out_dtype, o + 1, v.y / den);
+      store_out(a.out, a.out_dtype, o + 2, v.z / den);
+      store_out(a.out, a.out_dtype, o + 3, v.w / den);
+    }
+  }
+  if (tid == 0) {
+    if (a.cnt_out) a.cnt_out[h] = sm.red_i[0];
+    __hip_atomic_store(a.counter + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if constexpr (AHEAD) {
+    // Every workgroup of this head has read the index state and the labels (each counted itself
+    // in after its scan), so the state may now move to the next step: bin the keys that leave
+    // the window at length n + 1, as ssa_insert would at the start of the next step.
+    __syncthreads();                                     // the merge is done with sm.u
+    insert_phase<D>(sm.u.tail, a.st, a.ins, h, ipre, n + 1);
+  }
+}
+
+enum Mode { kDense = 0, kLabelled = 1, kFused = 2, kFusedAhead = 3 };
+
+
+template <typename T, int D, int GMAX>
+hipError_t launch_decode_t(const DecodeParams& p, int mode, hipStream_t st) {
+  dim3 grid(p.S, p.n_heads);
+  if (mode == kDense) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, true>), grid, dim3(kThreads), 0, st, p);
+  else if (mode == kLabelled) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false>), grid, dim3(kThreads), 0, st, p);
+  else if (mode == kFused) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true>), grid, dim3(kThreads), 0, st, p);
+  else hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true, true>), grid, dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_decode_d(const DecodeParams& p, int dense, hipStream_t st) {
+  if (p.G <= 1) return launch_decode_t<T, D, 1>(p, dense, st);
+  if (p.G <= 2) return launch_decode_t<T, D, 2>(p, dense, st);
+  if (p.G <= 4) return launch_decode_t<T, D, 4>(p, dense, st);
+  if (p.G <= 8) return launch_decode_t<T, D, 8>(p, dense, st);
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t launch_decode_ty(const DecodeParams& p, int d, int dense, hipStream_t st) {
+  switch (d) {
+    case 16: return launch_decode_d<T, 16>(p, dense, st);
+    case 32: return launch_decode_d<T, 32>(p, dense, st);
+    case 64: return launch_decode_d<T, 64>(p, dense, st);
+    case 128: return launch_decode_d<T, 128>(p, dense, st);
+    case 256: return launch_decode_d<T, 256>(p, dense, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+// One translation unit per KV dtype instantiates launch_decode_ty (decode_bf16.hip, decode_f16.hip,
+// decode_f32.hip), so the kernel variants compile in parallel.
+hipError_t launch_decode_bf16(const DecodeParams& p, int d, int mode, hipStream_t st);
+hipError_t launch_decode_f16(const DecodeParams& p, int d, int mode, hipStream_t st);
+hipError_t launch_decode_f32(const DecodeParams& p, int d, int mode, hipStream_t st);
+
+}  // namespace ssa

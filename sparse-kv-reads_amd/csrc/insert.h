@@ -1,0 +1,476 @@
+// Insertion of keys into their nearest cluster and the in-kernel split of a cluster that
+// passes its cap, for one (layer, sequence, KV head) per workgroup of kT threads. Used by the
+// insertion kernel (index.hip) and by the tail of the fused decode step (decode.h).
+//
+// Reference behaviour:
+//   insertion  _bin_kernel / _bin_dev_kernel    src/ssa/kernels/sphere_fused.py:171-227,
+//                                               src/ssa/kernels/graph_kernels.py:63-130
+//   split      _split_cluster                   src/ssa/kernels/sphere_fused.py:49-167
+//              (rule of _bisect_padded,         src/ssa/attn/sphere_gpu.py:76-102)
+// Every decision is made in the canonical arithmetic of ssa_common.h.
+#pragma once
+
+#include "select.h"
+
+namespace ssa {
+
+constexpr int kT = 256;       // threads per workgroup
+constexpr int kW = kT / 64;   // waves
+constexpr int kTile = 16;     // member rows staged in LDS by the split's ordered sums
+
+// LDS of the insertion and split code. A kernel that runs them passes a struct with the members
+// of InsertSmem (its own may add more to the union u, which must hold spl).
+struct SplitTile {
+  float tile[kTile][kMaxD];
+  int tside[kTile];
+};
+
+struct InsertBase {
+  float mu[kMaxD], kr[kMaxD], kn[kMaxD], sd[kMaxD];
+  float va[kMaxD], vb[kMaxD], vs[kMaxD];
+  float red_f[kW];
+  int red_i[kW];
+  float scal[4];
+  int scali[4];
+  float rmx, rmn;          // summaries of the cluster a key joins
+  int rcnt;
+};
+
+struct InsertSmem : InsertBase {
+  union {
+    SplitTile spl;
+  } u;
+};
+
+__device__ __forceinline__ int elem_size(int dt) { return dt == kF32 ? 4 : 2; }
+
+// ---- workgroup reductions (results are uniform across the workgroup) -----------------------
+
+template <class SM>
+__device__ __forceinline__ void block_argmax(SM& S, float& s, int& i) {
+  wave_argmax(s, i);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { S.red_f[w] = s; S.red_i[w] = i; }
+  __syncthreads();
+  s = S.red_f[0]; i = S.red_i[0];
+  for (int w2 = 1; w2 < kW; ++w2) argmax_merge(s, i, S.red_f[w2], S.red_i[w2]);
+  __syncthreads();
+}
+
+template <class SM>
+__device__ __forceinline__ void block_argmin(SM& S, float& s, int& i) {
+  wave_argmin(s, i);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { S.red_f[w] = s; S.red_i[w] = i; }
+  __syncthreads();
+  s = S.red_f[0]; i = S.red_i[0];
+  for (int w2 = 1; w2 < kW; ++w2) argmin_merge(s, i, S.red_f[w2], S.red_i[w2]);
+  __syncthreads();
+}
+
+template <class SM>
+__device__ __forceinline__ float block_max(SM& S, float v) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) S.red_f[w] = v;
+  __syncthreads();
+  float r = S.red_f[0];
+  for (int w2 = 1; w2 < kW; ++w2) r = fmaxf(r, S.red_f[w2]);
+  __syncthreads();
+  return r;
+}
+
+template <class SM>
+__device__ __forceinline__ int block_sum_i(SM& S, int v) {
+  v = wave_sum_i(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) S.red_i[w] = v;
+  __syncthreads();
+  int r = 0;
+  for (int w2 = 0; w2 < kW; ++w2) r += S.red_i[w2];
+  __syncthreads();
+  return r;
+}
+
+// Canonical unit vector of an LDS vector x (d entries) written to y (may alias x).
+template <class SM>
+__device__ __forceinline__ void block_unit(SM& S, const float* x, float* y, int d) {
+  if (threadIdx.x < 64) {
+    const float r = fmaxf(sqrtf(wave_cdot(x, x, d)), 1e-12f);
+    if (threadIdx.x == 0) S.scal[3] = r;
+  }
+  __syncthreads();
+  const float r = S.scal[3];
+  if (threadIdx.x < d) y[threadIdx.x] = x[threadIdx.x] / r;
+  __syncthreads();
+}
+
+// Key rows of one head's cache, element type T: element i of position p.
+template <typename T>
+struct KeysT {
+  const T* base; int64_t s_kn;
+  __device__ __forceinline__ float operator()(int p, int i) const { return to_f32(base[(int64_t)p * s_kn + i]); }
+};
+
+// Key rows of one head's cache, element type given at run time: element i of position p.
+struct Keys {
+  const char* base; int dt; int64_t s_kn;
+  __device__ float operator()(int p, int i) const { return load_as_f32(base, dt, (int64_t)p * s_kn + i); }
+};
+
+// ---- in-kernel split (rule of _bisect_padded) ----------------------------------------------
+
+// cdot with the loop over 8-element steps kept rolled (the split's operands are computed per
+// element from the key cache, and unrolled copies of that would hold many registers).
+template <typename FA, typename FB>
+__device__ __forceinline__ float cdot_rolled(FA a, FB b, int d) {
+  float c0 = 0.f, c1 = 0.f, c2 = 0.f, c3 = 0.f, c4 = 0.f, c5 = 0.f, c6 = 0.f, c7 = 0.f;
+#pragma unroll 1
+  for (int i = 0; i < d; i += 8) {
+    c0 = __builtin_fmaf(a(i + 0), b(i + 0), c0);
+    c1 = __builtin_fmaf(a(i + 1), b(i + 1), c1);
+    c2 = __builtin_fmaf(a(i + 2), b(i + 2), c2);
+    c3 = __builtin_fmaf(a(i + 3), b(i + 3), c3);
+    c4 = __builtin_fmaf(a(i + 4), b(i + 4), c4);
+    c5 = __builtin_fmaf(a(i + 5), b(i + 5), c5);
+    c6 = __builtin_fmaf(a(i + 6), b(i + 6), c6);
+    c7 = __builtin_fmaf(a(i + 7), b(i + 7), c7);
+  }
+  return ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7));
+}
+
+// Ordered sums over the members of the cluster being split: for each dimension i (thread i),
+// s1 = sum of kn_j[i] over members on side 1 and s0 over side 0, left to right in member order.
+template <class SM>
+__device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K, int m, float* s0_out, float* s1_out,
+                            int& n1_out) {
+  const int tid = threadIdx.x, d = H.d;
+  float s0 = 0.f, s1 = 0.f;
+  int n1 = 0;
+  for (int t0 = 0; t0 < m; t0 += kTile) {
+    const int nr = min(kTile, m - t0);
+    for (int e = tid; e < nr * d; e += kT) {
+      const int r = e / d, i = e % d, j = t0 + r;
+      const float magc = fmaxf(H.smag[j], 1e-12f);
+      S.u.spl.tile[r][i] = (K(H.mem[j], i) - S.mu[i]) / magc;
+    }
+    if (tid < nr) S.u.spl.tside[tid] = H.side[t0 + tid];
+    __syncthreads();
+    if (tid < d) {
+      for (int r = 0; r < nr; ++r) {
+        const float x = S.u.spl.tile[r][tid];
+        if (S.u.spl.tside[r]) { s1 = s1 + x; ++n1; } else { s0 = s0 + x; }
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < d) { s0_out[tid] = s0; s1_out[tid] = s1; }
+  if (tid == 0) S.scali[1] = n1;
+  __syncthreads();
+  n1_out = S.scali[1];
+  __syncthreads();
+}
+
+// side_j = kn_j.b > kn_j.a for every member (canonical dots), stored in H.side; returns #side 1.
+template <class SM>
+__device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K, int m, bool with_proj) {
+  const int tid = threadIdx.x, d = H.d;
+  int n1 = 0;
+  for (int j = tid; j < m; j += kT) {
+    const int pos = H.mem[j];
+    const float magc = fmaxf(H.smag[j], 1e-12f);
+    auto kn = [&](int i) { return (K(pos, i) - S.mu[i]) / magc; };
+    const float da = cdot_rolled(kn, [&](int i) { return S.va[i]; }, d);
+    const float db = cdot_rolled(kn, [&](int i) { return S.vb[i]; }, d);
+    const int one = db > da ? 1 : 0;
+    H.side[j] = one;
+    n1 += one;
+    if (with_proj) H.proj[j] = cdot_rolled(kn, [&](int i) { return S.vs[i]; }, d);
+  }
+  return block_sum_i(S, n1);
+}
+
+// Inlined (a call would put the caller's arguments and frame in scratch, whose set-up costs
+// every launch of the kernel); its dot loops stay rolled to keep registers down.
+template <class SM>
+__device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st, const Head& H, const Keys& K, int h,
+                              int c, int nw, int stop) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = H.d;
+  // 1. members in ascending position order
+  int m = 0;
+  for (int j0 = 1; j0 < stop; j0 += kT) {
+    const int j = j0 + tid;
+    const bool hit = j < stop && H.labels[j] == c;
+    const int incl = wave_prefix_count(hit, lane);
+    if (lane == 63) S.red_i[wave] = incl;
+    __syncthreads();
+    int wb = 0, tot = 0;
+    for (int w2 = 0; w2 < kW; ++w2) { if (w2 < wave) wb += S.red_i[w2]; tot += S.red_i[w2]; }
+    const int slot = m + wb + incl - 1;
+    if (hit && slot < H.ms) H.mem[slot] = j;
+    m += tot;
+    __syncthreads();
+  }
+  m = min(m, H.ms);
+  if (m < 2) return;   // labels and counts disagree: leave the cluster as it is
+  // 2. lengths
+  for (int j = tid; j < m; j += kT) {
+    const int pos = H.mem[j];
+    auto kr = [&](int i) { return K(pos, i) - S.mu[i]; };
+    H.smag[j] = sqrtf(cdot_rolled(kr, kr, d));
+  }
+  __syncthreads();
+  // 3. start from the first member and the member least similar to it
+  if (tid < d) S.va[tid] = (K(H.mem[0], tid) - S.mu[tid]) / fmaxf(H.smag[0], 1e-12f);
+  __syncthreads();
+  float lo = 0.f;
+  int far = -1;
+  for (int j = tid; j < m; j += kT) {
+    const int pos = H.mem[j];
+    const float magc = fmaxf(H.smag[j], 1e-12f);
+    auto kn = [&](int i) { return (K(pos, i) - S.mu[i]) / magc; };
+    argmin_merge(lo, far, cdot_rolled(kn, [&](int i) { return S.va[i]; }, d), j);
+  }
+  block_argmin(S, lo, far);
+  if (tid < d) S.vb[tid] = (K(H.mem[far], tid) - S.mu[tid]) / fmaxf(H.smag[far], 1e-12f);
+  __syncthreads();
+  // 4. 2-means on cosine similarity, 4 iterations
+  int n1 = 0;
+  for (int it = 0; it < 4; ++it) {
+    member_sides(S, H, K, m, false);
+    __syncthreads();
+    member_sums(S, H, K, m, S.kr, S.sd, n1);
+    if (m - n1 > 0) block_unit(S, S.kr, S.va, d);
+    if (n1 > 0) block_unit(S, S.sd, S.vb, d);
+  }
+  // 5. final sides and projections on b - a
+  if (tid < d) S.vs[tid] = S.vb[tid] - S.va[tid];
+  __syncthreads();
+  n1 = member_sides(S, H, K, m, true);
+  const float mf = (float)m, n1f = (float)n1;
+  if (n1f < 0.25f * mf || n1f > 0.75f * mf) {
+    // lopsided: cut at the median projection (rank ties by member order)
+    const int half = m / 2;
+    for (int j = tid; j < m; j += kT) {
+      const float pj = H.proj[j];
+      int rank = 0;
+      for (int i = 0; i < m; ++i) {
+        const float pi = H.proj[i];
+        rank += (pi < pj || (pi == pj && i < j)) ? 1 : 0;
+      }
+      H.side[j] = rank >= half ? 1 : 0;
+    }
+    __syncthreads();
+  }
+  // 6. both halves' summaries; relabel side 1
+  member_sums(S, H, K, m, S.kr, S.sd, n1);
+  float x0 = 0.f, x1 = 0.f, y0 = INFINITY, y1 = INFINITY;
+  for (int j = tid; j < m; j += kT) {
+    const float mg = H.smag[j];
+    if (H.side[j]) { x1 = fmaxf(x1, mg); y1 = fminf(y1, mg); H.labels[H.mem[j]] = (int16_t)nw; }
+    else { x0 = fmaxf(x0, mg); y0 = fminf(y0, mg); }
+  }
+  x0 = block_max(S, x0);
+  x1 = block_max(S, x1);
+  y0 = -block_max(S, -y0);
+  y1 = -block_max(S, -y1);
+  const int64_t r0 = (int64_t)c * d, r1 = (int64_t)nw * d;
+  if (tid < d) { H.sum_dir[r0 + tid] = S.kr[tid]; H.sum_dir[r1 + tid] = S.sd[tid]; }
+  block_unit(S, S.kr, S.va, d);
+  block_unit(S, S.sd, S.vb, d);
+  if (tid < d) {
+    H.cent[r0 + tid] = S.va[tid];
+    H.cent[r1 + tid] = S.vb[tid];
+    if (H.dir8) { H.dir8[r0 + tid] = q8(S.va[tid]); H.dir8[r1 + tid] = q8(S.vb[tid]); }
+    if (H.cent8) { H.cent8[r0 + tid] = q8(S.va[tid]); H.cent8[r1 + tid] = q8(S.vb[tid]); }
+  }
+  if (tid == 0) {
+    H.mmax[c] = x0; H.mmax[nw] = x1;
+    H.mmin[c] = y0; H.mmin[nw] = y1;
+    H.count[c] = m - n1; H.count[nw] = n1;
+    st.n_c[h] = nw + 1;
+    st.nsplit[h] = st.nsplit[h] + 1;
+  }
+  __syncthreads();
+}
+
+// ---- insertion ---------------------------------------------------------------------------
+
+// What an insertion reads before it knows the cluster a key joins, loaded in one round: the
+// head's scalars, element threadIdx.x of the centring mean, of the running key sum and of the key
+// at the expected position (the one that leaves the window when one key leaves per step), and
+// the centroid row and summaries of cluster threadIdx.x.
+template <int D>
+struct InsPre {
+  int old_end, n_act, flags;
+  float cap, vthr, rbar;
+  float mu, ks, kv;
+  int4 c8[D / 16];
+  int cnt;
+  float mx, mn;
+};
+
+__device__ __forceinline__ Keys head_keys_of(const ssa_index_state_t& st, const ssa_insert_args_t& in, int h) {
+  const int hpl = st.heads_per_layer;
+  const int layer = h / hpl;
+  Keys K;
+  K.dt = in.k_dtype;
+  K.s_kn = in.s_kn;
+  K.base = reinterpret_cast<const char*>(in.k) +
+           (int64_t)elem_size(in.k_dtype) * ((in.koff ? in.koff[layer] : 0) + (int64_t)(h % hpl) * in.s_kh);
+  return K;
+}
+
+// Expected position of the key to insert at length n: the last one of [end, max(n - window, 1)).
+__device__ __forceinline__ int expected_key(const ssa_insert_args_t& in, int n) { return max(n - in.window, 1) - 1; }
+
+template <int D>
+__device__ __forceinline__ void insert_prefetch(InsPre<D>& P, const ssa_index_state_t& st, const ssa_insert_args_t& in,
+                                                int h, int n) {
+  const int tid = threadIdx.x;
+  const Head H = head_view(st, h);
+  P.old_end = st.end[h];
+  P.n_act = st.n_c[h];
+  P.flags = st.flags[h];
+  P.cap = st.cap[h];
+  P.vthr = st.vthr[h];
+  P.rbar = st.rbar[h];
+  P.mu = 0.f; P.ks = 0.f; P.kv = 0.f;
+  if (tid < D) {
+    P.mu = st.mu_ref[(int64_t)h * D + tid];
+    P.ks = st.ksum[(int64_t)h * D + tid];
+    P.kv = head_keys_of(st, in, h)(expected_key(in, n), tid);
+  }
+  P.cnt = 0; P.mx = 0.f; P.mn = 0.f;
+  if (tid < st.C) {
+    P.cnt = H.count[tid];
+    P.mx = H.mmax[tid];
+    P.mn = H.mmin[tid];
+    if (H.q8cent) {
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) P.c8[k] = reinterpret_cast<const int4*>(H.cent8 + (int64_t)tid * D)[k];
+    }
+  }
+}
+
+// Insert the keys of [end, max(n - window, 1)) of head h into their nearest clusters (lowest
+// index on ties), splitting a cluster that passes its cap, then update end and the drift /
+// reset flags. P holds insert_prefetch(st, in, h, n). With one key to insert (the usual decode
+// step) the only load after P is the joined cluster's fp32 direction sum.
+template <int D, class SM>
+__device__ __forceinline__ void insert_phase(SM& S, const ssa_index_state_t& st, const ssa_insert_args_t& in, int h,
+                             const InsPre<D>& P, int n) {
+  const int tid = threadIdx.x, wave = tid >> 6, C = st.C;
+  const Head H = head_view(st, h);
+  const int old_end = P.old_end;
+  const int new_end = max(max(n - in.window, 1), old_end);
+  const int p_pre = expected_key(in, n);
+  const Keys K = head_keys_of(st, in, h);
+  const float mu_i = P.mu;
+  float ks_i = P.ks;
+  if (tid < D) S.mu[tid] = mu_i;
+  int n_act = P.n_act;
+  const float cap = P.cap, vthr = P.vthr;
+  __syncthreads();
+  for (int p = old_end; p < new_end && n_act > 0; ++p) {
+    const bool first = p == old_end;          // nothing written yet: the prefetched rows are current
+    if (tid < D) {
+      const float kv = p == p_pre ? P.kv : K(p, tid);
+      ks_i = ks_i + kv;
+      S.kr[tid] = kv - mu_i;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const float mag = sqrtf(wave_cdot(S.kr, S.kr, D));
+      if (tid == 0) S.scal[0] = mag;
+    }
+    __syncthreads();
+    const float mag = S.scal[0];
+    const float magc = fmaxf(mag, 1e-12f);
+    if (tid < D) S.kn[tid] = S.kr[tid] / magc;
+    __syncthreads();
+    float best = 0.f;
+    int bi = -1;
+    const float (*kn)[kMaxD] = reinterpret_cast<const float (*)[kMaxD]>(S.kn);
+    // canonical dots <cent_c, kn> (the row's self-dot comes along unused); cluster threadIdx.x
+    // first, from its prefetched row on the first key (outside the loop, so that the row's
+    // conversion is not hoisted into registers for every iteration)
+    if (tid < n_act) {
+      float nrm2, sc[1];
+      if (H.q8cent && first) {
+        int4 raw[D / 16];
+#pragma unroll
+        for (int k = 0; k < D / 16; ++k) {
+          raw[k] = P.c8[k];
+          asm volatile("" : "+v"(raw[k].x), "+v"(raw[k].y), "+v"(raw[k].z), "+v"(raw[k].w));   // not hoisted
+        }
+        row_dots_raw<D, 1>(raw, kn, 1, nrm2, sc);
+      } else if (H.q8cent) {
+        row_dots<D, 1>(H.cent8 + (int64_t)tid * D, kn, 1, nrm2, sc);
+      } else {
+        row_dots<D, 1>(H.cent + (int64_t)tid * D, kn, 1, nrm2, sc);
+      }
+      argmax_merge(best, bi, sc[0], tid);
+    }
+    for (int c = tid + kT; c < n_act; c += kT) {
+      float nrm2, sc[1];
+      if (H.q8cent) row_dots<D, 1>(H.cent8 + (int64_t)c * D, kn, 1, nrm2, sc);
+      else row_dots<D, 1>(H.cent + (int64_t)c * D, kn, 1, nrm2, sc);
+      argmax_merge(best, bi, sc[0], c);
+    }
+    block_argmax(S, best, bi);
+    const int row = bi;
+    if (tid < D) {
+      const float sd = H.sum_dir[(int64_t)row * D + tid] + S.kn[tid];
+      H.sum_dir[(int64_t)row * D + tid] = sd;
+      S.sd[tid] = sd;
+    }
+    // the joined cluster's summaries: from its thread's prefetch, else from memory
+    const bool held = first && row < kT;
+    if (held && tid == row) { S.rmx = P.mx; S.rmn = P.mn; S.rcnt = P.cnt; }
+    if (!held && tid == 0) { S.rmx = H.mmax[row]; S.rmn = H.mmin[row]; S.rcnt = H.count[row]; }
+    __syncthreads();
+    if (wave == 0) {
+      const float sdsq = wave_cdot(S.sd, S.sd, D);
+      if (tid == 0) {
+        S.scal[1] = sqrtf(sdsq);
+        H.mmax[row] = fmaxf(S.rmx, mag);
+        H.mmin[row] = fminf(S.rmn, mag);
+        const int cn = S.rcnt + 1;
+        H.count[row] = cn;
+        H.labels[p] = (int16_t)row;
+        const float cnf = (float)cn;
+        const bool wide = (1.0f - sdsq / (cnf * cnf) > vthr) && (cn >= in.var_min);
+        const bool over = cnf > fmaxf(cap, in.capk * (float)p);
+        S.scali[0] = ((over || wide) && n_act < C && cn >= 2 && cn <= H.ms) ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    if (H.dir8 && tid < D) H.dir8[(int64_t)row * D + tid] = q8(S.sd[tid] / fmaxf(S.scal[1], 1e-12f));
+    if (S.scali[0]) {
+      __syncthreads();
+      split_cluster(S, st, H, K, h, row, n_act, p + 1);
+      n_act += 1;
+    }
+    __syncthreads();
+  }
+  // running mean vs the centring mean: drift flag; cluster count: reset flag
+  const float nb = (float)(new_end - 1);
+  if (tid < D) {
+    st.ksum[(int64_t)h * D + tid] = ks_i;
+    S.vs[tid] = ks_i / fmaxf(nb, 1.f) - mu_i;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float dist = sqrtf(wave_cdot(S.vs, S.vs, D));
+    if (tid == 0) {
+      const bool moved = (dist > in.delta * P.rbar) && (nb > 0.f);
+      st.flags[h] = P.flags | (moved ? 1 : 0) | ((n_act >= in.reset_at) ? 2 : 0);
+      st.end[h] = new_end;
+      S.scali[2] = new_end;
+    }
+  }
+  __syncthreads();
+}
+
+}  // namespace ssa

@@ -71,29 +71,39 @@ __device__ __forceinline__ void load_row(const float* r, float (&x)[D]) {
   }
 }
 
-// Canonical dot of two LDS vectors, computed by the calling wave (lanes 0..7 run the eight
-// chains, shuffles combine them in the canonical tree); every lane of the wave gets the result.
+// Canonical dot of two LDS vectors, computed by the calling wave: lanes 0..7 run the eight
+// chains, then DPP moves combine them in the canonical tree (lane 0 adds lane 1, then lanes 2-3,
+// then lane 7, which holds (c4+c5)+(c6+c7) by then); the result is read from lane 0, so every
+// lane of the wave gets it. The whole wave must be active.
 __device__ __forceinline__ float wave_cdot(const float* a, const float* b, int d) {
   const int lane = threadIdx.x & 63;
   float c = 0.f;
   if (lane < 8)
     for (int i = lane; i < d; i += 8) c = __builtin_fmaf(a[i], b[i], c);
-  const float p = c + __shfl_xor(c, 1, 64);
-  const float q = p + __shfl_xor(p, 2, 64);
-  const float r = q + __shfl_xor(q, 4, 64);
-  return __shfl(r, 0, 64);
+  c = c + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0xB1, 0xF, 0xF, true));   // lane ^ 1
+  c = c + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x4E, 0xF, 0xF, true));   // lane ^ 2
+  c = c + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0x141, 0xF, 0xF, true));  // 7 - lane
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(c)));
 }
 
-// Canonical dots of one cluster row with itself (nrm2) and with the G query rows held in LDS
-// (dot[g]), all in one pass over the row, 16 elements at a time: chain j of every dot takes
-// elements j, j+8, j+16, ... in increasing order, as cdot does, so the results are identical.
-// int8 rows are loaded whole (one 16-byte load per 16 elements) before any use.
+// Canonical dots of one cluster row with itself (nrm2) and with the GMAX query rows held in LDS
+// (dot[g]; rows g >= G of q are zero and their dots unused), all in one pass over the row, 16
+// elements at a time: chain j of every dot takes elements j, j+8, j+16, ... in increasing order,
+// as cdot does, so the results are identical. int8 rows are loaded whole (one 16-byte load per
+// 16 elements) before any use.
+// An offset of 0 the compiler cannot see through: loads through a pointer moved by it are not
+// hoisted out of loops or merged across calls, so a row of LDS that many loop iterations read
+// is read per use instead of being held in registers.
+__device__ __forceinline__ int opaque_zero() {
+  int z = 0;
+  asm volatile("" : "+v"(z));
+  return z;
+}
+
 template <int D, int GMAX>
-__device__ __forceinline__ void row_dots(const int8_t* r, const float (*q)[kMaxD], int G, float& nrm2,
-                                         float (&dot)[GMAX]) {
-  int4 raw[D / 16];
-#pragma unroll
-  for (int k = 0; k < D / 16; ++k) raw[k] = reinterpret_cast<const int4*>(r)[k];
+__device__ __forceinline__ void row_dots_raw(const int4 (&raw)[D / 16], const float (*q0)[kMaxD], int G, float& nrm2,
+                                             float (&dot)[GMAX]) {
+  const float (*q)[kMaxD] = q0 + opaque_zero();
   float cn[8], cq[GMAX][8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -111,8 +121,7 @@ __device__ __forceinline__ void row_dots(const int8_t* r, const float (*q)[kMaxD
       const int j = e % 8, i = 16 * k + e;
       cn[j] = __builtin_fmaf(x, x, cn[j]);
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) cq[g][j] = __builtin_fmaf(q[g][i], x, cq[g][j]);
+      for (int g = 0; g < GMAX; ++g) cq[g][j] = __builtin_fmaf(q[g][i], x, cq[g][j]);
     }
   }
   nrm2 = ((cn[0] + cn[1]) + (cn[2] + cn[3])) + ((cn[4] + cn[5]) + (cn[6] + cn[7]));
@@ -122,8 +131,18 @@ __device__ __forceinline__ void row_dots(const int8_t* r, const float (*q)[kMaxD
 }
 
 template <int D, int GMAX>
-__device__ __forceinline__ void row_dots(const float* r, const float (*q)[kMaxD], int G, float& nrm2,
+__device__ __forceinline__ void row_dots(const int8_t* r, const float (*q)[kMaxD], int G, float& nrm2,
                                          float (&dot)[GMAX]) {
+  int4 raw[D / 16];
+#pragma unroll
+  for (int k = 0; k < D / 16; ++k) raw[k] = reinterpret_cast<const int4*>(r)[k];
+  row_dots_raw<D, GMAX>(raw, q, G, nrm2, dot);
+}
+
+template <int D, int GMAX>
+__device__ __forceinline__ void row_dots(const float* r, const float (*q0)[kMaxD], int G, float& nrm2,
+                                         float (&dot)[GMAX]) {
+  const float (*q)[kMaxD] = q0 + opaque_zero();
   float cn[8], cq[GMAX][8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -145,8 +164,7 @@ __device__ __forceinline__ void row_dots(const float* r, const float (*q)[kMaxD]
       const int j = e % 8, i = 16 * k + e;
       cn[j] = __builtin_fmaf(x[e], x[e], cn[j]);
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) cq[g][j] = __builtin_fmaf(q[g][i], x[e], cq[g][j]);
+      for (int g = 0; g < GMAX; ++g) cq[g][j] = __builtin_fmaf(q[g][i], x[e], cq[g][j]);
     }
   }
   nrm2 = ((cn[0] + cn[1]) + (cn[2] + cn[3])) + ((cn[4] + cn[5]) + (cn[6] + cn[7]));
@@ -155,85 +173,157 @@ __device__ __forceinline__ void row_dots(const float* r, const float (*q)[kMaxD]
     dot[g] = ((cq[g][0] + cq[g][1]) + (cq[g][2] + cq[g][3])) + ((cq[g][4] + cq[g][5]) + (cq[g][6] + cq[g][7]));
 }
 
+constexpr int kBins = 1024;     // threshold buckets of the selection (top 10 bits of the rank key)
+
 template <int GMAX>
 struct SelSmem {
-  float q[GMAX][kMaxD];     // the group's query rows, fp32
-  float z[GMAX][kMaxC];     // scores, then softmax terms
-  float key[kMaxC];         // ranking key per slot
-  int cnt[kMaxC];           // keys per live slot (0 otherwise)
-  float tree[GMAX][1];      // softmax denominators
-  unsigned long long rk[kMaxC];   // rank keys: (score descending, index ascending) as one integer
-  float red[GMAX][16];
+  float q[GMAX][kMaxD];             // the group's query rows, fp32
+  float z[GMAX][kMaxC];             // softmax terms, for the denominator tree
+  float tree[GMAX];                 // softmax denominators
+  float red[GMAX][16];              // per-wave maxima
+  int hist[kBins];                  // keys per bucket
+  int wsum[16];                     // per-wave bucket totals
+  int bstar, base, nlist;           // crossing bucket, keys ranked before it, its member count
+  unsigned long long lrk[kMaxC];    // rank keys of the crossing bucket's clusters
+  int lcnt[kMaxC];                  // and their key counts
 };
 
-// Per-row maxima over the slots of S.z[0..nrow): one pass, one pair of barriers.
-template <int NT, int GMAX>
-__device__ __forceinline__ void sel_row_max(SelSmem<GMAX>& S, int nrow, int C, float (&out)[GMAX]) {
-  const int w = threadIdx.x >> 6;
+// The state a thread scores first (slot threadIdx.x), loaded at kernel start so that its
+// memory latency overlaps the query and label loads.
+template <int D>
+struct SelPre {
+  int4 raw[D / 16];                 // int8 direction row (8-bit summaries only)
+  int cnt;
+  float mx, mn;
+};
+
+template <int D>
+__device__ __forceinline__ void sel_prefetch(SelPre<D>& P, const Head& H, int C) {
+  const int c = threadIdx.x;
+  P.cnt = 0; P.mx = 0.f; P.mn = 0.f;
+  if (c < C) {
+    P.cnt = H.count[c];
+    P.mx = H.mmax[c];
+    P.mn = H.mmin[c];
+    if (H.q8dirs) {
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    if (g >= nrow) break;
-    float v = -INFINITY;
-    for (int c = threadIdx.x; c < C; c += NT) v = fmaxf(v, S.z[g][c]);
-    v = wave_max(v);
-    if ((threadIdx.x & 63) == 0) S.red[g][w] = v;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    if (g >= nrow) break;
-    float r = S.red[g][0];
-    for (int w2 = 1; w2 < NT / 64; ++w2) r = fmaxf(r, S.red[g][w2]);
-    out[g] = r;
+      for (int k = 0; k < D / 16; ++k) P.raw[k] = reinterpret_cast<const int4*>(H.dir8 + (int64_t)c * D)[k];
+    }
   }
 }
 
-// Integer rank key of a score: ascending order of the key is (score desc, slot asc); -0 and +0
-// compare equal (x + 0 maps -0 to +0), -inf (dead slots) sorts after every finite score.
-__device__ __forceinline__ unsigned long long rank_key(float key, int c) {
+// Orderable bits of a key for the selection order: ascending bits = descending key; -0 and +0
+// are one key (x + 0 maps -0 to +0); -inf sorts after every finite key.
+__device__ __forceinline__ unsigned int desc_bits(float key) {
   const unsigned int u = __float_as_uint(key + 0.0f);
   const unsigned int asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)(~asc) << 32) | (unsigned int)c;
+  return ~asc;
 }
 
-// Take cluster c iff it is live and the live clusters ranked before it, by (key desc, index
-// asc), hold fewer than `need` keys. Slots past n_act have key -inf and count 0.
-template <int NT, int GMAX, typename Emit>
-__device__ __forceinline__ void rank_take(SelSmem<GMAX>& S, const float* key, int n_act, int C, int64_t need,
-                                          int row, Emit emit) {
-  for (int c = threadIdx.x; c < C; c += NT) S.rk[c] = rank_key(key[c], c);
-  __syncthreads();
-  const int jn = min(C, (n_act + 15) & ~15);
-  for (int c = threadIdx.x; c < C; c += NT) {
-    const bool live = c < n_act && S.cnt[c] > 0;
-    const unsigned long long kc = S.rk[c];
-    int before = 0;
-    for (int j0 = 0; j0 < jn; j0 += 16) {
-      // 16 slots per step: every LDS read of the step is issued before the compares
-      unsigned long long k[16];
-      int n[16];
+// Integer rank key of (key, slot): ascending order is (key desc, slot asc).
+__device__ __forceinline__ unsigned long long rank_key(float key, int c) {
+  return ((unsigned long long)desc_bits(key) << 32) | (unsigned int)c;
+}
+
+// Take cluster c iff it is live (cnt > 0) and the live clusters ranked before it, by (key desc,
+// index asc), hold fewer than `need` keys: before(c) < need.
+// Exact threshold search instead of a full ranking: bucket b(c) = top 10 bits of the rank key
+// is monotone in the rank order, so with b* the first bucket where the running key count
+// reaches need and base the count of all buckets before b*, every cluster of a bucket before b*
+// has before(c) <= base - cnt(c) < need (taken), every cluster of a bucket after b* has
+// before(c) >= base + count(b*) >= need (not taken), and a cluster of bucket b* has
+// before(c) = base + (its bucket's clusters ranked before it), counted exactly. If all keys
+// together are fewer than need, every live cluster is taken.
+// On entry S.hist is zero and S.nlist is 0; both are so again on return.
+template <int NT, int KPT, int GMAX, typename Emit>
+__device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)[KPT], const int (&cnt)[KPT], int C,
+                                            int64_t need, int row, Emit emit) {
+  static_assert(kBins == 4 * NT, "one int4 of buckets per thread");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  unsigned int db[KPT];
 #pragma unroll
-      for (int e = 0; e < 16; e += 4) {
-        const int4 c4 = *reinterpret_cast<const int4*>(S.cnt + j0 + e);
-        n[e] = c4.x; n[e + 1] = c4.y; n[e + 2] = c4.z; n[e + 3] = c4.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) k[e] = S.rk[j0 + e];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) before += k[e] < kc ? n[e] : 0;
-    }
-    emit(row, c, (live && (int64_t)before < need) ? 1.f : 0.f);
+  for (int k = 0; k < KPT; ++k) {
+    db[k] = desc_bits(key[k]);
+    if (cnt[k] > 0) atomicAdd(&S.hist[db[k] >> 22], cnt[k]);
   }
   __syncthreads();
+  const int4 hb = reinterpret_cast<const int4*>(S.hist)[tid];
+  const int own = hb.x + hb.y + hb.z + hb.w;
+  int incl = own;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) S.wsum[wave] = incl;
+  __syncthreads();
+  int wbase = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    const int v = S.wsum[w];
+    if (w < wave) wbase += v;
+    total += v;
+  }
+  const int64_t lo = wbase + incl - own, hi = wbase + incl;
+  if (lo < need && need <= hi) {            // the crossing lies in this thread's four buckets
+    const int v[4] = {hb.x, hb.y, hb.z, hb.w};
+    int64_t cum = lo;
+    int b = 4 * tid + 3;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (cum + v[e] >= need) { b = 4 * tid + e; break; }
+      cum += v[e];
+    }
+    S.bstar = b;
+    S.base = (int)cum;
+  }
+  if (tid == NT - 1 && (int64_t)total < need) { S.bstar = kBins; S.base = total; }
+  reinterpret_cast<int4*>(S.hist)[tid] = make_int4(0, 0, 0, 0);     // this thread's buckets, read above
+  __syncthreads();
+  const unsigned int bstar = (unsigned int)S.bstar;
+  const int64_t base = S.base;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    if (cnt[k] > 0 && (db[k] >> 22) == bstar) {
+      const int i = atomicAdd(&S.nlist, 1);
+      S.lrk[i] = ((unsigned long long)db[k] << 32) | (unsigned int)(tid + k * NT);
+      S.lcnt[i] = cnt[k];
+    }
+  }
+  __syncthreads();
+  const int nl = S.nlist;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    const int c = tid + k * NT;
+    if (c >= C) break;
+    float x = 0.f;
+    if (cnt[k] > 0) {
+      const unsigned int b = db[k] >> 22;
+      if (b < bstar) {
+        x = 1.f;
+      } else if (b == bstar) {
+        const unsigned long long rk = ((unsigned long long)db[k] << 32) | (unsigned int)c;
+        int64_t before = base;
+        for (int i = 0; i < nl; ++i) before += S.lrk[i] < rk ? S.lcnt[i] : 0;
+        x = before < need ? 1.f : 0.f;
+      }
+    }
+    emit(row, c, x);
+  }
+  __syncthreads();
+  if (tid == 0) S.nlist = 0;
 }
 
-// Selection for one head. S.q must hold the G query rows (fp32) and be visible (barrier) on
-// entry. emit(row, c, w) receives w for every slot c in [0, C] of every weight row (one row, or
-// G rows for per_head); slot C, the always-read exact set, gets 1.
+// Selection for one head. S.q must hold the G query rows (fp32), rows G..GMAX-1 zero, and be
+// visible (barrier) on entry; P holds slot threadIdx.x's state (sel_prefetch). emit(row, c, w) receives w for every
+// slot c in [0, C] of every weight row (one row, or G rows for per_head); slot C, the
+// always-read exact set, gets 1. Each thread scores slots threadIdx.x + k * NT and keeps their
+// scores in registers.
 template <int D, int NT, int GMAX, typename Emit>
-__device__ void select_head(SelSmem<GMAX>& S, const Head& H, int C, int n_act, int end, int G, double budget,
-                            int group, float scale, Emit emit) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, const SelPre<D>& P, int C, int n_act, int end, int G,
+                            double budget, int group, float scale, Emit emit) {
+  constexpr int KPT = kMaxC / NT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool per_head = group == 1;
   const int nrows = per_head ? G : 1;
   const int nb = end - 1;
@@ -245,46 +335,92 @@ __device__ void select_head(SelSmem<GMAX>& S, const Head& H, int C, int n_act, i
       for (int c = tid; c < C; c += NT) emit(r, c, 0.f);
     return;
   }
-  for (int c = tid; c < C; c += NT) {
-    // every load of this slot is issued before the first use
-    const bool used = c < n_act;
-    const int cnt = used ? H.count[c] : 0;
+  reinterpret_cast<int4*>(S.hist)[tid] = make_int4(0, 0, 0, 0);
+  if (tid == 0) S.nlist = 0;
+  // scores e[g] = (p >= 0 ? mmax : mmin) * p, p = q_g . dir / |dir|, scaled by 1/sqrt(d) unless per_head
+  float z[KPT][GMAX];
+  int cnt[KPT];
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    const int c = tid + k * NT;
+    const bool used = c < C && c < n_act;
     float mx = 0.f, mn = 0.f, nrm2 = 0.f, dot[GMAX];
-    if (used) {
-      mx = H.mmax[c];
-      mn = H.mmin[c];
+    int ct = 0;
+    if (k == 0) {
+      ct = P.cnt; mx = P.mx; mn = P.mn;
+      if (used) {
+        if (H.q8dirs) row_dots_raw<D, GMAX>(P.raw, S.q, G, nrm2, dot);
+        else row_dots<D, GMAX>(H.sum_dir + (int64_t)c * D, S.q, G, nrm2, dot);
+      }
+    } else if (used) {
+      ct = H.count[c]; mx = H.mmax[c]; mn = H.mmin[c];
       if (H.q8dirs) row_dots<D, GMAX>(H.dir8 + (int64_t)c * D, S.q, G, nrm2, dot);
       else row_dots<D, GMAX>(H.sum_dir + (int64_t)c * D, S.q, G, nrm2, dot);
     }
-    const bool live = cnt > 0;
-    S.cnt[c] = live ? cnt : 0;
-    if (live) {
-      const float nrm = fmaxf(sqrtf(nrm2), 1e-12f);
+    cnt[k] = used && ct > 0 ? ct : 0;
+    const float nrm = fmaxf(sqrtf(nrm2), 1e-12f);
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g) {
-        if (g >= G) break;
+    for (int g = 0; g < GMAX; ++g) {
+      float e = -INFINITY;
+      if (cnt[k] > 0 && g < G) {
         const float p = dot[g] / nrm;
-        const float e = p >= 0.f ? mx * p : mn * p;
-        S.z[g][c] = per_head ? e : e * scale;
+        e = p >= 0.f ? mx * p : mn * p;
+        if (!per_head) e = e * scale;
       }
-    } else {
-      for (int g = 0; g < G; ++g) S.z[g][c] = -INFINITY;
+      z[k][g] = e;
     }
   }
-  __syncthreads();
   if (per_head) {
-    for (int g = 0; g < G; ++g) rank_take<NT>(S, S.z[g], n_act, C, need, g, emit);
+    __syncthreads();                          // S.hist / S.nlist cleared
+    for (int g = 0; g < G; ++g) {
+      float key[KPT];
+#pragma unroll
+      for (int k = 0; k < KPT; ++k) {
+        key[k] = -INFINITY;
+#pragma unroll
+        for (int g2 = 0; g2 < GMAX; ++g2)
+          if (g2 == g) key[k] = z[k][g2];
+      }
+      bucket_take<NT, KPT>(S, key, cnt, C, need, g, emit);
+    }
     return;
   }
+  // per-head maxima over live clusters (sum_share, max_rel)
   float zmx[GMAX];
+  if (group == 0 || group == 3) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < KPT; ++k) v = fmaxf(v, z[k][g]);
+      v = wave_max(v);
+      if (lane == 0 && g < G) S.red[g][wave] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      float r = -INFINITY;
+      if (g < G) {
+        r = S.red[g][0];
+        for (int w2 = 1; w2 < NT / 64; ++w2) r = fmaxf(r, S.red[g][w2]);
+      }
+      zmx[g] = r;
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) zmx[g] = 0.f;
+  }
+  float key[KPT];
   if (group == 0) {
-    // sum_share: per head a softmax over live clusters, summed over the heads (all heads at once)
-    sel_row_max<NT>(S, G, C, zmx);
-    for (int c = tid; c < C; c += NT) {
+    // sum_share: per head a softmax over live clusters, summed over the heads
+    float t[KPT][GMAX];
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
+      const int c = tid + k * NT;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
-        if (g >= G) break;
-        S.z[g][c] = S.cnt[c] > 0 ? cexp(S.z[g][c] - zmx[g]) : 0.f;
+        t[k][g] = (cnt[k] > 0 && g < G) ? cexp(z[k][g] - zmx[g]) : 0.f;
+        if (g < G && c < C) S.z[g][c] = t[k][g];
       }
     }
     __syncthreads();
@@ -293,48 +429,44 @@ __device__ void select_head(SelSmem<GMAX>& S, const Head& H, int C, int n_act, i
     // strides >= 64 of the tree, then the strides 32 .. 1 run as shuffles. The terms are >= 0,
     // so padding with +0 and folding from the largest stride gives the same bits as the tree
     // over exactly C slots.
-    {
-      const int w = tid >> 6, lane = tid & 63;
-      for (int g = w; g < G; g += NT / 64) {
-        float t[kMaxC / 64];
+    for (int g = wave; g < G; g += NT / 64) {
+      float u[kMaxC / 64];
 #pragma unroll
-        for (int k = 0; k < kMaxC / 64; ++k) t[k] = (lane + 64 * k < C) ? S.z[g][lane + 64 * k] : 0.f;
+      for (int k = 0; k < kMaxC / 64; ++k) u[k] = (lane + 64 * k < C) ? S.z[g][lane + 64 * k] : 0.f;
 #pragma unroll
-        for (int half = kMaxC / 128; half >= 1; half >>= 1)
+      for (int half = kMaxC / 128; half >= 1; half >>= 1)
 #pragma unroll
-          for (int k = 0; k < half; ++k) t[k] = t[k] + t[k + half];
-        float v = t[0];
+        for (int k = 0; k < half; ++k) u[k] = u[k] + u[k + half];
+      float v = u[0];
 #pragma unroll
-        for (int h = 32; h >= 1; h >>= 1) {
-          const float o = __shfl_down(v, h, 64);
-          if (lane < h) v = v + o;
-        }
-        if (lane == 0) S.tree[g][0] = v;
+      for (int hh = 32; hh >= 1; hh >>= 1) {
+        const float o = __shfl_down(v, hh, 64);
+        if (lane < hh) v = v + o;
       }
+      if (lane == 0) S.tree[g] = v;
     }
     __syncthreads();
-    for (int c = tid; c < C; c += NT) {
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
       float s = 0.f;
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g) {
-        if (g >= G) break;
-        s = s + S.z[g][c] / S.tree[g][0];
-      }
-      S.key[c] = S.cnt[c] > 0 ? s : -INFINITY;
+      for (int g = 0; g < GMAX; ++g)
+        if (g < G) s = s + t[k][g] / S.tree[g];
+      key[k] = cnt[k] > 0 ? s : -INFINITY;
     }
   } else {
     // max / max_rel
-    if (group == 3) sel_row_max<NT>(S, G, C, zmx);
-    else
-      for (int g = 0; g < GMAX; ++g) zmx[g] = 0.f;
-    for (int c = tid; c < C; c += NT) {
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
       float s = -INFINITY;
-      for (int g = 0; g < G; ++g) s = fmaxf(s, S.z[g][c] - zmx[g]);
-      S.key[c] = S.cnt[c] > 0 ? s : -INFINITY;
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g)
+        if (g < G) s = fmaxf(s, z[k][g] - zmx[g]);
+      key[k] = cnt[k] > 0 ? s : -INFINITY;
     }
+    __syncthreads();                          // S.hist / S.nlist cleared
   }
-  __syncthreads();
-  rank_take<NT>(S, S.key, n_act, C, need, 0, emit);
+  bucket_take<NT, KPT>(S, key, cnt, C, need, 0, emit);
 }
 
 }  // namespace ssa

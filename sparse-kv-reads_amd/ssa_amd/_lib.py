@@ -92,7 +92,8 @@ ENTRY_POINTS = {
     "ssa_insert": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(InsertArgs), vp]),
     "ssa_select": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(InsertArgs), ct.POINTER(SelectArgs), vp]),
     "ssa_build": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(BuildArgs), vp]),
-    "ssa_sparse_step": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs), vp]),
+    "ssa_sparse_step": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs),
+                                   ct.POINTER(InsertArgs), vp]),
 }
 
 _lib = None

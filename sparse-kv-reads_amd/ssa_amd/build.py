@@ -1,9 +1,9 @@
 """Build libssa_hip.so (the HIP kernels and their C ABI) for gfx950, in the package directory.
 
-Both sources are compiled with ``-ffp-contract=off``: the selection and insertion decisions
-(select.h, shared by both files) must be reproducible bit for bit, and the attention loops
-spell out their fused multiply-adds. Both are linked into one shared library next to this
-file, which ``ssa_amd._lib`` loads.
+Every source is compiled with ``-ffp-contract=off``: the selection and insertion decisions
+(select.h, shared by the decode and index kernels) must be reproducible bit for bit, and the
+attention loops spell out their fused multiply-adds. The sources compile in parallel and are
+linked into one shared library next to this file, which ``ssa_amd._lib`` loads.
 """
 
 from __future__ import annotations
@@ -11,6 +11,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -23,7 +24,8 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
           # packed fp32 instructions are kept out of every kernel
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-fhip-fp32-correctly-rounded-divide-sqrt", f"-I{INCLUDE}"]
-SOURCES = {"attention.hip": ["-ffp-contract=off"], "index.hip": ["-ffp-contract=off"]}
+SOURCES = {name: ["-ffp-contract=off"] for name in
+           ("decode_bf16.hip", "decode_f16.hip", "decode_f32.hip", "attention.hip", "index.hip")}
 
 
 def _hipcc() -> str:
@@ -45,14 +47,16 @@ def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     objdir = PKG / "_obj"
     objdir.mkdir(exist_ok=True)
-    objs = []
+    cmds, objs = [], []
     for src, extra in SOURCES.items():
         obj = objdir / (src.replace(".hip", ".o"))
-        cmd = [hipcc, *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        _run(cmd)
+        cmds.append([hipcc, *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
+        if verbose:
+            print(" ".join(cmds[-1]), flush=True)
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(_run, cmds))
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, "-shared", f"--offload-arch={ARCH}", *objs, "-o", str(tmp)])
     os.replace(tmp, LIB)

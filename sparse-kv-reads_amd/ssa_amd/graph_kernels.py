@@ -7,11 +7,13 @@ inside the selection kernel.
 
 Mirrors src/ssa/kernels/graph_kernels.py:
   * ``DenseAttentionGraph`` (:171-189): exact split-K decode over ``[0, n)``, one launch.
-  * ``SphereIndexGraph`` (:192-279): per step two launches, ``ssa_insert`` (binning of the key
-    that left the window, in-kernel split of an over-cap cluster) and ``ssa_sparse_step`` (each
-    workgroup scores the clusters and takes the selection in LDS, scans the labels, runs
-    split-K attention over the selected rows, and the last workgroup of a head merges the
-    splits), where the reference issues bin, score, pick, zero, compact, list and merge.
+  * ``SphereIndexGraph`` (:192-279): per step one launch, ``ssa_sparse_step``: each workgroup
+    scores the clusters and takes the selection in LDS, scans the labels and runs split-K
+    attention over the selected rows; the last workgroup of a head merges the splits and then
+    bins the key that leaves the window at the next step (in-kernel split included), which the
+    reference bins at the start of that step. The reference issues bin, score, pick, zero,
+    compact, list and merge. With ``insert_ahead=False`` the binning is a launch of its own
+    (``ssa_insert``) before the step's, as in the reference.
   * ``AllLayerInsert`` (:286-325): one insertion launch for every layer.
 """
 
@@ -47,8 +49,9 @@ class SphereIndexGraph(SphereIndexFused):
     """``SphereIndexFused`` for graph capture: ``step`` issues only fixed-argument kernels."""
 
     def __init__(self, *, budget: float, block_n: int = 32, compact_block: int = 1024, refit_every: int = 0,
-                 num_splits: int | None = None, **kw):
+                 num_splits: int | None = None, insert_ahead: bool = True, **kw):
         super().__init__(**kw)
+        self.insert_ahead = insert_ahead
         self.refit_every = refit_every
         self.refits = 0
         self.budget = budget
@@ -57,8 +60,14 @@ class SphereIndexGraph(SphereIndexFused):
 
     def prepare(self, K: torch.Tensor, n: int, H: int) -> None:
         """Build from the prefilled cache ``K [H_kv, capacity, d]`` holding ``n`` positions (eager,
-        outside the graph) and allocate the step's fixed buffers."""
+        outside the graph) and allocate the step's fixed buffers. With ``insert_ahead`` the keys
+        that leave the window at length ``n + 1`` are binned too: every step's launch leaves the
+        state binned for the next length, so ``step`` must be called at ``n + 1``, ``n + 2``, ..."""
         self.observe(K, n)
+        if self.insert_ahead and max(1, n + 1 - self.window) > self.end:
+            check(lib().ssa_insert(self._state(), self._insert_args(K, n_host=n + 1), stream_ptr(self.device)),
+                  "ssa_insert")
+            self.end = max(1, n + 1 - self.window)
         H_kv, d, dev = self.H_kv, self.d, self.device
         self.G = H // H_kv
         self.end_dev.fill_(self.end)
@@ -75,16 +84,20 @@ class SphereIndexGraph(SphereIndexFused):
 
     def step(self, q, K, V, n_dev, insert: bool = True):
         """One decode step; ``K, V [H_kv, capacity, d]`` with position ``n - 1`` already written.
-        ``insert=False`` when the keys leaving the window were already inserted for every layer
-        by one launch (``AllLayerInsert``). Launches: ``ssa_insert`` (unless ``insert=False``) and
-        ``ssa_sparse_step`` (selection and attention); ``wbuf`` receives the selection."""
+        With ``insert_ahead`` one launch, ``ssa_sparse_step``, which also bins the keys for the
+        next step. Otherwise ``ssa_insert`` (unless ``insert=False``: the keys leaving the window
+        were already inserted for every layer by one launch, ``AllLayerInsert``) and then
+        ``ssa_sparse_step``. ``wbuf`` receives the selection."""
         s = stream_ptr(q.device)
         st = self._state()
-        if insert:
+        ahead = None
+        if self.insert_ahead:
+            ahead = self._insert_args(K)
+        elif insert:
             check(lib().ssa_insert(st, self._insert_args(K, n_dev=n_dev), s), "ssa_insert")
         sel = self._select_args(q, self.wbuf, self.budget, "sum_share")
         a = attn_args(q, K, V, self.out, self.work, labels=self.labels, w=self.wbuf, n_dev=n_dev)
-        check(lib().ssa_sparse_step(st, sel, a, s), "ssa_sparse_step")
+        check(lib().ssa_sparse_step(st, sel, a, ahead, s), "ssa_sparse_step")
         return self.out
 
     def _host_end(self) -> None:

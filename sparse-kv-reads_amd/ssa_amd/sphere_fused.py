@@ -61,6 +61,8 @@ def kmeans_init_indices(m: int, C: int, seed: int) -> torch.Tensor:
 
 
 class SphereIndexFused:
+    BUILD_HEADS = 64          # heads (re)built per ssa_build call
+
     def __init__(self, *, C: int = 256, window: int = 64, delta: float = 0.03, capacity: int = 65536,
                  check_every: int = 16, seed: int = 0, kind: str = "random", partition: str = "random",
                  kmeans_iters: int = 10, C_init: int | None = None, split_factor: float = 0.0,
@@ -182,13 +184,13 @@ class SphereIndexFused:
             return
         todo = [h for h in hl if self.partition == "kmeans" and not self.fitted[h]]
         keep = [h for h in hl if h not in todo]
+        pos = {h: i for i, h in enumerate(hl)}
         for group, fit in ((todo, True), (keep, False)):
-            if group:
-                sel_mu = None
-                if mu is not None:
-                    pos = {h: i for i, h in enumerate(hl)}
-                    sel_mu = mu[[pos[h] for h in group]].to(torch.float32).contiguous()
-                self._build_heads(K, group, sel_mu, fit)
+            # at most BUILD_HEADS heads per pass: the scratch is ~2 x heads x keys x d fp32
+            for i in range(0, len(group), self.BUILD_HEADS):
+                part = group[i:i + self.BUILD_HEADS]
+                sel_mu = None if mu is None else mu[[pos[h] for h in part]].to(torch.float32).contiguous()
+                self._build_heads(K, part, sel_mu, fit)
 
     def _build_heads(self, K, heads: list[int], mu, fit: bool) -> None:
         dev, d, C = self.device, self.d, self.C
@@ -387,8 +389,8 @@ class SphereIndexFused:
         work = _work(self.H_kv, S, H // self.H_kv, d, q.device)
         out = torch.empty(H, d, device=q.device, dtype=q.dtype)
         a = attn_args(q, K, V, out, work, labels=self.labels, w=w, n_host=n, per_head=group == "per_head")
-        check(lib().ssa_sparse_step(self._state(), self._select_args(q, w, budget, group), a, stream_ptr(q.device)),
-              "ssa_sparse_step")
+        check(lib().ssa_sparse_step(self._state(), self._select_args(q, w, budget, group), a, None,
+                                    stream_ptr(q.device)), "ssa_sparse_step")
         return out, self.labels[:, :n], w
 
     # -- counters ------------------------------------------------------------------------------
