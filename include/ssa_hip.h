@@ -94,7 +94,11 @@ typedef struct ssa_index_state {
   int32_t* nsplit;          /* [n_heads] splits done in kernels */
   int16_t* labels;          /* [n_heads, capacity] */
   int32_t* mem; float* proj; int32_t* side; float* smag;   /* [n_heads, ms] split scratch */
+  int32_t* stage;           /* [n_heads, SSA_STAGE_WORDS] insertion staged by ssa_sparse_step's
+                               insert-ahead workgroup, committed by the head's last workgroup */
 } ssa_index_state_t;
+
+#define SSA_STAGE_WORDS 80  /* 8 header words + up to 256 int8 direction values */
 
 typedef struct ssa_insert_args {
   const void* k; int32_t k_dtype; int64_t s_kh; int64_t s_kn;   /* cache of the first layer */

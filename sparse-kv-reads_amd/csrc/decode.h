@@ -160,275 +160,281 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   const int s0 = min(sp * chunk, n);
   const int s1 = min(s0 + chunk, n);
   const int16_t* labrow = DENSE ? nullptr : a.labels + (int64_t)h * a.s_lh;
-
-  // Issue the selection state's and the first page's label loads before anything waits on memory.
-  SelPre<D> pre;
-  if constexpr (SELECT) sel_prefetch<D>(pre, head_view(a.st, h), a.st.C);
-  int lbl[PER];
-  if constexpr (!DENSE) {
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int j = s0 + u * kThreads + tid;
-      lbl[u] = j < s1 ? (int)labrow[j] : 0;
+  // AHEAD: workgroup S of each head (one past the splits) stages the next step's insertion
+  const bool stager = AHEAD && sp == S;
+  if (stager) {
+    InsPre<AHEAD ? D : 16> spre;
+    if constexpr (AHEAD) {
+      insert_prefetch<D>(spre, a.st, a.ins, h, n + 1);
+      insert_stage<D>(sm.u.tail, a.st, a.ins, h, spre, n + 1);
     }
-  }
-
-  // q rows of the group: one uniform dtype branch, then 16-byte loads (rows 16-byte aligned)
-  float qr[GMAX][8];
+  } else {
+    // Issue the selection state's and the first page's label loads before anything waits on memory.
+    SelPre<D> pre;
+    if constexpr (SELECT) sel_prefetch<D>(pre, head_view(a.st, h), a.st.C);
+    int lbl[PER];
+    if constexpr (!DENSE) {
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    const int64_t off = (int64_t)(h * G + min(g, G - 1)) * a.s_qh + li * 8;
-    float r[8];
-    if (a.q_dtype == kBF16) widen8(*reinterpret_cast<const uint4*>(reinterpret_cast<const __hip_bfloat16*>(a.q) + off), r, (__hip_bfloat16*)nullptr);
-    else if (a.q_dtype == kF16) widen8(*reinterpret_cast<const uint4*>(reinterpret_cast<const __half*>(a.q) + off), r, (__half*)nullptr);
-    else {
-      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.q) + off);
-      const float4 x = p[0], y = p[1];
-      r[0] = x.x; r[1] = x.y; r[2] = x.z; r[3] = x.w; r[4] = y.x; r[5] = y.y; r[6] = y.z; r[7] = y.w;
+      for (int u = 0; u < PER; ++u) {
+        const int j = s0 + u * kThreads + tid;
+        lbl[u] = j < s1 ? (int)labrow[j] : 0;
+      }
     }
+
+    // q rows of the group: one uniform dtype branch, then 16-byte loads (rows 16-byte aligned)
+    float qr[GMAX][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qr[g][e] = g < G ? r[e] * a.qscale : 0.f;
+    for (int g = 0; g < GMAX; ++g) {
+      const int64_t off = (int64_t)(h * G + min(g, G - 1)) * a.s_qh + li * 8;
+      float r[8];
+      if (a.q_dtype == kBF16) widen8(*reinterpret_cast<const uint4*>(reinterpret_cast<const __hip_bfloat16*>(a.q) + off), r, (__hip_bfloat16*)nullptr);
+      else if (a.q_dtype == kF16) widen8(*reinterpret_cast<const uint4*>(reinterpret_cast<const __half*>(a.q) + off), r, (__half*)nullptr);
+      else {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.q) + off);
+        const float4 x = p[0], y = p[1];
+        r[0] = x.x; r[1] = x.y; r[2] = x.z; r[3] = x.w; r[4] = y.x; r[5] = y.y; r[6] = y.z; r[7] = y.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qr[g][e] = g < G ? r[e] * a.qscale : 0.f;
+      if constexpr (SELECT) {
+        // lane group 0 of wave 0 holds the whole row: the selection's fp32 copy (rows >= G zero)
+        if (wave == 0 && lg == 0) {
+          float4* dst = reinterpret_cast<float4*>(&sm.u.sel.q[g][li * 8]);
+          dst[0] = g < G ? make_float4(r[0], r[1], r[2], r[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+          dst[1] = g < G ? make_float4(r[4], r[5], r[6], r[7]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+
     if constexpr (SELECT) {
-      // lane group 0 of wave 0 holds the whole row: the selection's fp32 copy (rows >= G zero)
-      if (wave == 0 && lg == 0) {
-        float4* dst = reinterpret_cast<float4*>(&sm.u.sel.q[g][li * 8]);
-        dst[0] = g < G ? make_float4(r[0], r[1], r[2], r[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
-        dst[1] = g < G ? make_float4(r[4], r[5], r[6], r[7]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      // the head's selection, computed here while the label loads are in flight
+      const int n_act = a.st.n_c[h], end = a.st.end[h];
+      __syncthreads();
+      float* wout = const_cast<float*>(a.w);
+      const int64_t s_wr = a.s_wr;
+      const bool store_w = sp == 0 && wout != nullptr;
+      select_head<D, kThreads, GMAX>(sm.u.sel, head_view(a.st, h), pre, a.st.C, n_act, end, G, a.budget, a.group,
+                                     a.sel_scale, [&](int r, int c, float x) {
+                                       sm.lw[r][c] = x > 0.f ? 0.f : -INFINITY;
+                                       if (store_w) wout[(int64_t)(per_head ? h * G + r : h) * s_wr + c] = x;
+                                     });
+    } else if constexpr (!DENSE) {
+      const int nrow = per_head ? G : 1;
+      for (int r = 0; r < nrow; ++r) {
+        const float* wr = a.w + (int64_t)(per_head ? h * G + r : h) * a.s_wr;
+        float x[(kMaxW + kThreads - 1) / kThreads];
+#pragma unroll
+        for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
+          const int c = tid + k * kThreads;
+          x[k] = c < a.w_len ? wr[c] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
+          const int c = tid + k * kThreads;
+          if (c < a.w_len) sm.lw[r][c] = x[k] > 0.f ? __log2f(x[k]) : -INFINITY;
+        }
       }
     }
-  }
 
-  if constexpr (SELECT) {
-    // the head's selection, computed here while the label loads are in flight
-    const int n_act = a.st.n_c[h], end = a.st.end[h];
-    __syncthreads();
-    float* wout = const_cast<float*>(a.w);
-    const int64_t s_wr = a.s_wr;
-    const bool store_w = sp == 0 && wout != nullptr;
-    select_head<D, kThreads, GMAX>(sm.u.sel, head_view(a.st, h), pre, a.st.C, n_act, end, G, a.budget, a.group,
-                                   a.sel_scale, [&](int r, int c, float x) {
-                                     sm.lw[r][c] = x > 0.f ? 0.f : -INFINITY;
-                                     if (store_w) wout[(int64_t)(per_head ? h * G + r : h) * s_wr + c] = x;
-                                   });
-  } else if constexpr (!DENSE) {
-    const int nrow = per_head ? G : 1;
-    for (int r = 0; r < nrow; ++r) {
-      const float* wr = a.w + (int64_t)(per_head ? h * G + r : h) * a.s_wr;
-      float x[(kMaxW + kThreads - 1) / kThreads];
+    float m_[GMAX], l_[GMAX], acc[GMAX][8];
 #pragma unroll
-      for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
-        const int c = tid + k * kThreads;
-        x[k] = c < a.w_len ? wr[c] : 0.f;
-      }
+    for (int g = 0; g < GMAX; ++g) {
+      m_[g] = kNeg;
+      l_[g] = 0.f;
 #pragma unroll
-      for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
-        const int c = tid + k * kThreads;
-        if (c < a.w_len) sm.lw[r][c] = x[k] > 0.f ? __log2f(x[k]) : -INFINITY;
-      }
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
     }
-  }
 
-  float m_[GMAX], l_[GMAX], acc[GMAX][8];
+    const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)h * a.s_kh + li * 8;
+    const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)h * a.s_vh + li * 8;
+    int rows_read = 0;
+
+    for (int p0 = s0; p0 < s1; p0 += kPage) {
+      const int pn = min(kPage, s1 - p0);
+      int R;
+      if constexpr (DENSE) {
+        R = pn;
+      } else {
+        if (p0 != s0) {
 #pragma unroll
-  for (int g = 0; g < GMAX; ++g) {
-    m_[g] = kNeg;
-    l_[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  }
-
-  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)h * a.s_kh + li * 8;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)h * a.s_vh + li * 8;
-  int rows_read = 0;
-
-  for (int p0 = s0; p0 < s1; p0 += kPage) {
-    const int pn = min(kPage, s1 - p0);
-    int R;
-    if constexpr (DENSE) {
-      R = pn;
-    } else {
-      if (p0 != s0) {
+          for (int u = 0; u < PER; ++u) {
+            const int j = p0 + u * kThreads + tid;
+            lbl[u] = j < s1 ? (int)labrow[j] : 0;
+          }
+        }
+        __syncthreads();   // lw ready / previous page's list consumed
+        // Position p0 + u * kThreads + tid: the list in (u, wave, lane) order is ascending.
+        bool sel[PER];
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-          const int j = p0 + u * kThreads + tid;
-          lbl[u] = j < s1 ? (int)labrow[j] : 0;
-        }
-      }
-      __syncthreads();   // lw ready / previous page's list consumed
-      // Position p0 + u * kThreads + tid: the list in (u, wave, lane) order is ascending.
-      bool sel[PER];
-#pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        const int j = u * kThreads + tid;
-        lbl[u] = min(max(lbl[u], 0), a.w_len - 1);     // a bad label never indexes outside lw
-        bool s = false;
-        if (j < pn) {
-          if (per_head) {
-            for (int g = 0; g < G; ++g) s |= sm.lw[g][lbl[u]] != -INFINITY;
-          } else {
-            s = sm.lw[0][lbl[u]] != -INFINITY;
+          const int j = u * kThreads + tid;
+          lbl[u] = min(max(lbl[u], 0), a.w_len - 1);     // a bad label never indexes outside lw
+          bool s = false;
+          if (j < pn) {
+            if (per_head) {
+              for (int g = 0; g < G; ++g) s |= sm.lw[g][lbl[u]] != -INFINITY;
+            } else {
+              s = sm.lw[0][lbl[u]] != -INFINITY;
+            }
           }
+          sel[u] = s;
         }
-        sel[u] = s;
-      }
-      const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-      unsigned long long bal[PER];
+        const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        unsigned long long bal[PER];
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        bal[u] = __ballot(sel[u]);
-        if (lane == 0) sm.scan[u][wave] = __popcll(bal[u]);
-      }
-      __syncthreads();
-      int total = 0;
-#pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        int wbase = 0, tot_u = 0;
-#pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
-          const int c2 = sm.scan[u][w2];
-          if (w2 < wave) wbase += c2;
-          tot_u += c2;
+        for (int u = 0; u < PER; ++u) {
+          bal[u] = __ballot(sel[u]);
+          if (lane == 0) sm.scan[u][wave] = __popcll(bal[u]);
         }
-        if (sel[u]) {
-          const int o = total + wbase + __popcll(bal[u] & below);
-          sm.u.list.pos[o] = p0 + u * kThreads + tid;
-          if (per_head) {
-            for (int g = 0; g < G; ++g) sm.u.list.rlw[g][o] = sm.lw[g][lbl[u]];
-          } else {
-            sm.u.list.rlw[0][o] = sm.lw[0][lbl[u]];
+        __syncthreads();
+        int total = 0;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          int wbase = 0, tot_u = 0;
+#pragma unroll
+          for (int w2 = 0; w2 < kWaves; ++w2) {
+            const int c2 = sm.scan[u][w2];
+            if (w2 < wave) wbase += c2;
+            tot_u += c2;
           }
+          if (sel[u]) {
+            const int o = total + wbase + __popcll(bal[u] & below);
+            sm.u.list.pos[o] = p0 + u * kThreads + tid;
+            if (per_head) {
+              for (int g = 0; g < G; ++g) sm.u.list.rlw[g][o] = sm.lw[g][lbl[u]];
+            } else {
+              sm.u.list.rlw[0][o] = sm.lw[0][lbl[u]];
+            }
+          }
+          total += tot_u;
         }
-        total += tot_u;
+        R = total;
+        __syncthreads();
       }
-      R = total;
-      __syncthreads();
-    }
-    rows_read += R;
+      rows_read += R;
 
-    // ---- attention over the R rows of this page: every lane group issues U rows of K and V,
-    // then consumes them; rows past R re-read the last row and are masked out.
-    for (int base = 0; base < R; base += kWaves * RPI * U) {
-      Raw kraw[U], vraw[U];
-      int rr[U];
+      // ---- attention over the R rows of this page: every lane group issues U rows of K and V,
+      // then consumes them; rows past R re-read the last row and are masked out.
+      for (int base = 0; base < R; base += kWaves * RPI * U) {
+        Raw kraw[U], vraw[U];
+        int rr[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        rr[u] = base + u * kWaves * RPI + wave * RPI + lg;
-        const int rc = min(rr[u], R - 1);
-        int pos;
-        if constexpr (DENSE) pos = p0 + rc;
-        else pos = sm.u.list.pos[rc];
-        kraw[u] = *reinterpret_cast<const Raw*>(kbase + (int64_t)pos * a.s_kn);
-        vraw[u] = *reinterpret_cast<const Raw*>(vbase + (int64_t)pos * a.s_vn);
-      }
-      float s[GMAX][U];
+        for (int u = 0; u < U; ++u) {
+          rr[u] = base + u * kWaves * RPI + wave * RPI + lg;
+          const int rc = min(rr[u], R - 1);
+          int pos;
+          if constexpr (DENSE) pos = p0 + rc;
+          else pos = sm.u.list.pos[rc];
+          kraw[u] = *reinterpret_cast<const Raw*>(kbase + (int64_t)pos * a.s_kn);
+          vraw[u] = *reinterpret_cast<const Raw*>(vbase + (int64_t)pos * a.s_vn);
+        }
+        float s[GMAX][U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float kf[8];
-        widen8(kraw[u], kf, (T*)nullptr);
-        float lw0 = 0.f;
-        if constexpr (!DENSE) lw0 = rr[u] < R ? sm.u.list.rlw[0][min(rr[u], R - 1)] : -INFINITY;
+        for (int u = 0; u < U; ++u) {
+          float kf[8];
+          widen8(kraw[u], kf, (T*)nullptr);
+          float lw0 = 0.f;
+          if constexpr (!DENSE) lw0 = rr[u] < R ? sm.u.list.rlw[0][min(rr[u], R - 1)] : -INFINITY;
+#pragma unroll
+          for (int g = 0; g < GMAX; ++g) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kf[e], d);
+            d = row_sum<LPR>(d);
+            float lw = lw0;
+            if constexpr (!DENSE) {
+              if (per_head && g < G) lw = rr[u] < R ? sm.u.list.rlw[g][min(rr[u], R - 1)] : -INFINITY;
+            }
+            s[g][u] = rr[u] < R ? d + lw : -INFINITY;
+          }
+        }
+        float p[GMAX][U];
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
-          float d = 0.f;
+          float mx = m_[g];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) d = fmaf(qr[g][e], kf[e], d);
-          d = row_sum<LPR>(d);
-          float lw = lw0;
-          if constexpr (!DENSE) {
-            if (per_head && g < G) lw = rr[u] < R ? sm.u.list.rlw[g][min(rr[u], R - 1)] : -INFINITY;
-          }
-          s[g][u] = rr[u] < R ? d + lw : -INFINITY;
+          for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[g][u]);
+          const float alpha = __builtin_amdgcn_exp2f(m_[g] - mx);
+          float psum = 0.f;
+#pragma unroll
+          for (int u = 0; u < U; ++u) { p[g][u] = __builtin_amdgcn_exp2f(s[g][u] - mx); psum += p[g][u]; }
+          l_[g] = fmaf(l_[g], alpha, psum);
+          m_[g] = mx;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float vf[8];
+          widen8(vraw[u], vf, (T*)nullptr);
+#pragma unroll
+          for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p[g][u], vf[e], acc[g][e]);
         }
       }
-      float p[GMAX][U];
+    }
+
+    // ---- merge the lane groups of each wave ---------------------------------------------------
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1) {
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
-        float mx = m_[g];
+        const float m2 = __shfl_xor(m_[g], o, 64);
+        const float l2 = __shfl_xor(l_[g], o, 64);
+        const float M = fmaxf(m_[g], m2);
+        const float f1 = __builtin_amdgcn_exp2f(m_[g] - M), f2 = __builtin_amdgcn_exp2f(m2 - M);
+        l_[g] = l_[g] * f1 + l2 * f2;
 #pragma unroll
-        for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[g][u]);
-        const float alpha = __builtin_amdgcn_exp2f(m_[g] - mx);
-        float psum = 0.f;
-#pragma unroll
-        for (int u = 0; u < U; ++u) { p[g][u] = __builtin_amdgcn_exp2f(s[g][u] - mx); psum += p[g][u]; }
-        l_[g] = fmaf(l_[g], alpha, psum);
-        m_[g] = mx;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float vf[8];
-        widen8(vraw[u], vf, (T*)nullptr);
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p[g][u], vf[e], acc[g][e]);
+        for (int e = 0; e < 8; ++e) {
+          const float a2 = __shfl_xor(acc[g][e], o, 64);
+          acc[g][e] = acc[g][e] * f1 + a2 * f2;
+        }
+        m_[g] = M;
       }
     }
-  }
+    if (lane < LPR) {
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) {
+        if (lane == 0) { sm.red_m[wave][g] = m_[g]; sm.red_l[wave][g] = l_[g]; }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.red_a[wave][g][li * 8 + e] = acc[g][e];
+      }
+    }
+    __syncthreads();
 
-  // ---- merge the lane groups of each wave ---------------------------------------------------
+    // ---- merge the waves; publish this workgroup's partial -------------------------------------
+    // Partials are written with agent-scope stores (coherent across the XCDs' L2 caches), so the
+    // workgroup only has to wait for its own stores before it counts itself in: no L2 write-back.
+    const int64_t pidx = (int64_t)h * S + sp;
+    for (int t = tid; t < G * D; t += kThreads) {
+      const int g = t / D, dd = t % D;
+      float M = kNeg;
 #pragma unroll
-  for (int o = LPR; o < 64; o <<= 1) {
+      for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, sm.red_m[w2][g]);
+      float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      const float m2 = __shfl_xor(m_[g], o, 64);
-      const float l2 = __shfl_xor(l_[g], o, 64);
-      const float M = fmaxf(m_[g], m2);
-      const float f1 = __builtin_amdgcn_exp2f(m_[g] - M), f2 = __builtin_amdgcn_exp2f(m2 - M);
-      l_[g] = l_[g] * f1 + l2 * f2;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a2 = __shfl_xor(acc[g][e], o, 64);
-        acc[g][e] = acc[g][e] * f1 + a2 * f2;
+      for (int w2 = 0; w2 < kWaves; ++w2) {
+        const float f = __builtin_amdgcn_exp2f(sm.red_m[w2][g] - M);
+        L = fmaf(sm.red_l[w2][g], f, L);
+        A = fmaf(sm.red_a[w2][g][dd], f, A);
       }
-      m_[g] = M;
+      __hip_atomic_store(a.part_a + (pidx * G + g) * D + dd, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (dd == 0) {
+        __hip_atomic_store(a.part_m + pidx * G + g, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.part_l + pidx * G + g, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-  }
-  if (lane < LPR) {
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-      if (lane == 0) { sm.red_m[wave][g] = m_[g]; sm.red_l[wave][g] = l_[g]; }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.red_a[wave][g][li * 8 + e] = acc[g][e];
-    }
-  }
-  __syncthreads();
-
-  // ---- merge the waves; publish this workgroup's partial -------------------------------------
-  // Partials are written with agent-scope stores (coherent across the XCDs' L2 caches), so the
-  // workgroup only has to wait for its own stores before it counts itself in: no L2 write-back.
-  const int64_t pidx = (int64_t)h * S + sp;
-  for (int t = tid; t < G * D; t += kThreads) {
-    const int g = t / D, dd = t % D;
-    float M = kNeg;
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves; ++w2) M = fmaxf(M, sm.red_m[w2][g]);
-    float L = 0.f, A = 0.f;
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves; ++w2) {
-      const float f = __builtin_amdgcn_exp2f(sm.red_m[w2][g] - M);
-      L = fmaf(sm.red_l[w2][g], f, L);
-      A = fmaf(sm.red_a[w2][g][dd], f, A);
-    }
-    __hip_atomic_store(a.part_a + (pidx * G + g) * D + dd, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (dd == 0) {
-      __hip_atomic_store(a.part_m + pidx * G + g, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.part_l + pidx * G + g, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (tid == 0) __hip_atomic_store(a.part_cnt + pidx, rows_read, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(a.part_cnt + pidx, rows_read, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }  // attention workgroups
   __builtin_amdgcn_s_waitcnt(0);       // this thread's stores have reached the coherence point
   __syncthreads();
   if (tid == 0) {
     const int old = __hip_atomic_fetch_add(a.counter + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm.last = (old == S - 1);
+    sm.last = (old == S - 1 + (AHEAD ? 1 : 0));
   }
   __syncthreads();
   if (!sm.last) return;
-  // the insertion ahead reads its state while the merge's loads are in flight
-  InsPre<AHEAD ? D : 16> ipre;
-  if constexpr (AHEAD) insert_prefetch<D>(ipre, a.st, a.ins, h, n + 1);
   // ---- the last workgroup of head h merges the S partials ----------------------------------
   // One round of loads, all issued before the first wait: this thread's accumulator columns
   // (up to kMergeBatch splits) into registers and, in wave 0, every split's (max, sum) and row
@@ -546,10 +552,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   }
   if constexpr (AHEAD) {
     // Every workgroup of this head has read the index state and the labels (each counted itself
-    // in after its scan), so the state may now move to the next step: bin the keys that leave
-    // the window at length n + 1, as ssa_insert would at the start of the next step.
+    // in after its scan, the stager after its stores), so the state may now move to the next
+    // step: commit the staged insertion of the keys that leave the window at length n + 1, as
+    // ssa_insert would bin them at the start of the next step.
     __syncthreads();                                     // the merge is done with sm.u
-    insert_phase<D>(sm.u.tail, a.st, a.ins, h, ipre, n + 1);
+    insert_commit<D>(sm.u.tail, a.st, a.ins, h, n + 1);
   }
 }
 
@@ -558,7 +565,7 @@ enum Mode { kDense = 0, kLabelled = 1, kFused = 2, kFusedAhead = 3 };
 
 template <typename T, int D, int GMAX>
 hipError_t launch_decode_t(const DecodeParams& p, int mode, hipStream_t st) {
-  dim3 grid(p.S, p.n_heads);
+  dim3 grid(p.S + (mode == kFusedAhead ? 1 : 0), p.n_heads);
   if (mode == kDense) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, true>), grid, dim3(kThreads), 0, st, p);
   else if (mode == kLabelled) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false>), grid, dim3(kThreads), 0, st, p);
   else if (mode == kFused) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true>), grid, dim3(kThreads), 0, st, p);

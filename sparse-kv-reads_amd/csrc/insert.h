@@ -34,6 +34,7 @@ struct InsertBase {
   int scali[4];
   float rmx, rmn;          // summaries of the cluster a key joins
   int rcnt;
+  int8_t d8[kMaxD];        // its new int8 direction, staged
 };
 
 struct InsertSmem : InsertBase {
@@ -471,6 +472,165 @@ __device__ __forceinline__ void insert_phase(SM& S, const ssa_index_state_t& st,
     }
   }
   __syncthreads();
+}
+
+// ---- insertion staged beside the decode step ------------------------------------------------
+//
+// ssa_sparse_step's insert-ahead workgroup prepares the insertion of the next step's key while
+// the attention workgroups of its head still read the index state: it writes what they do not
+// read (the joined cluster's fp32 direction sum, the running key sum) and stages the rest in
+// st.stage; the head's last workgroup, once every other one is done, commits the staged values
+// (and runs a split, or the general insertion when the step is not the usual one key).
+constexpr int kStageWords = SSA_STAGE_WORDS;
+constexpr int kStageHead = 12;       // header words before the int8 direction row
+enum StageStatus { kStageNone = 0, kStageOne = 1, kStageGeneral = 2, kStageSplit = 3 };
+// header: [0] status, [1] cluster, [2] position, [3] new end, [4] count, [5] mmax, [6] mmin,
+//         [7] clusters in use, [8] flags
+
+__device__ __forceinline__ void stage_put(int32_t* stg, int i, int v) {
+  __hip_atomic_store(stg + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int stage_get(const int32_t* stg, int i) {
+  return __hip_atomic_load(stg + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Stage the insertion at length n. Takes the one-key path when exactly the prefetched key
+// leaves the window and scoring reads the int8 directions; anything else is left to the commit
+// (kStageGeneral), which then runs insert_phase itself.
+template <int D, class SM>
+__device__ __forceinline__ void insert_stage(SM& S, const ssa_index_state_t& st, const ssa_insert_args_t& in, int h,
+                                             const InsPre<D>& P, int n) {
+  static_assert(kStageHead + D / 4 <= kStageWords, "stage row too short");
+  const int tid = threadIdx.x, wave = tid >> 6, C = st.C;
+  const Head H = head_view(st, h);
+  int32_t* stg = st.stage + (int64_t)h * kStageWords;
+  const int old_end = P.old_end;
+  const int new_end = max(max(n - in.window, 1), old_end);
+  const int n_act = P.n_act;
+  const int p = old_end;
+  if (!(new_end == old_end + 1 && n_act > 0 && H.q8dirs && p == expected_key(in, n))) {
+    if (tid == 0) stage_put(stg, 0, kStageGeneral);
+    return;
+  }
+  const float mu_i = P.mu;
+  float ks_i = P.ks;
+  if (tid < D) {
+    ks_i = ks_i + P.kv;
+    S.kr[tid] = P.kv - mu_i;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float mag = sqrtf(wave_cdot(S.kr, S.kr, D));
+    if (tid == 0) S.scal[0] = mag;
+  }
+  __syncthreads();
+  const float mag = S.scal[0];
+  const float magc = fmaxf(mag, 1e-12f);
+  if (tid < D) S.kn[tid] = S.kr[tid] / magc;
+  __syncthreads();
+  float best = 0.f;
+  int bi = -1;
+  const float (*kn)[kMaxD] = reinterpret_cast<const float (*)[kMaxD]>(S.kn);
+  if (tid < n_act) {
+    float nrm2, sc[1];
+    if (H.q8cent) {
+      int4 raw[D / 16];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) raw[k] = P.c8[k];
+      row_dots_raw<D, 1>(raw, kn, 1, nrm2, sc);
+    } else {
+      row_dots<D, 1>(H.cent + (int64_t)tid * D, kn, 1, nrm2, sc);
+    }
+    argmax_merge(best, bi, sc[0], tid);
+  }
+  for (int c = tid + kT; c < n_act; c += kT) {
+    float nrm2, sc[1];
+    if (H.q8cent) row_dots<D, 1>(H.cent8 + (int64_t)c * D, kn, 1, nrm2, sc);
+    else row_dots<D, 1>(H.cent + (int64_t)c * D, kn, 1, nrm2, sc);
+    argmax_merge(best, bi, sc[0], c);
+  }
+  block_argmax(S, best, bi);
+  const int row = bi;
+  if (tid < D) {
+    const float sd = H.sum_dir[(int64_t)row * D + tid] + S.kn[tid];
+    H.sum_dir[(int64_t)row * D + tid] = sd;       // the attention reads only the int8 copy
+    S.sd[tid] = sd;
+  }
+  if (row < kT && tid == row) { S.rmx = P.mx; S.rmn = P.mn; S.rcnt = P.cnt; }
+  if (row >= kT && tid == 0) { S.rmx = H.mmax[row]; S.rmn = H.mmin[row]; S.rcnt = H.count[row]; }
+  __syncthreads();
+  if (wave == 0) {
+    const float sdsq = wave_cdot(S.sd, S.sd, D);
+    if (tid == 0) {
+      S.scal[1] = sqrtf(sdsq);
+      const int cn = S.rcnt + 1;
+      const float cnf = (float)cn;
+      const bool wide = (1.0f - sdsq / (cnf * cnf) > P.vthr) && (cn >= in.var_min);
+      const bool over = cnf > fmaxf(P.cap, in.capk * (float)p);
+      const bool split = (over || wide) && n_act < C && cn >= 2 && cn <= H.ms;
+      stage_put(stg, 0, split ? kStageSplit : kStageOne);
+      stage_put(stg, 1, row);
+      stage_put(stg, 2, p);
+      stage_put(stg, 3, new_end);
+      stage_put(stg, 4, cn);
+      stage_put(stg, 5, __float_as_int(fmaxf(S.rmx, mag)));
+      stage_put(stg, 6, __float_as_int(fminf(S.rmn, mag)));
+      stage_put(stg, 7, n_act);
+    }
+  }
+  __syncthreads();
+  if (tid < D) S.d8[tid] = q8(S.sd[tid] / fmaxf(S.scal[1], 1e-12f));
+  // running mean vs the centring mean: drift flag; cluster count: reset flag
+  const float nb = (float)(new_end - 1);
+  if (tid < D) {
+    st.ksum[(int64_t)h * D + tid] = ks_i;
+    S.vs[tid] = ks_i / fmaxf(nb, 1.f) - mu_i;
+  }
+  __syncthreads();
+  if (tid < D / 4) stage_put(stg, kStageHead + tid, reinterpret_cast<const int*>(S.d8)[tid]);
+  if (wave == 0) {
+    const float dist = sqrtf(wave_cdot(S.vs, S.vs, D));
+    if (tid == 0) {
+      const bool moved = (dist > in.delta * P.rbar) && (nb > 0.f);
+      stage_put(stg, 8, P.flags | (moved ? 1 : 0) | ((n_act >= in.reset_at) ? 2 : 0));
+    }
+  }
+}
+
+// Commit what insert_stage staged for head h (called by the head's last workgroup, after every
+// workgroup of the step has read the state). A kStageGeneral stage runs the whole insertion.
+template <int D, class SM>
+__device__ __forceinline__ void insert_commit(SM& S, const ssa_index_state_t& st, const ssa_insert_args_t& in, int h,
+                                              int n) {
+  const int tid = threadIdx.x;
+  const Head H = head_view(st, h);
+  const int32_t* stg = st.stage + (int64_t)h * kStageWords;
+  const int status = stage_get(stg, 0);
+  if (status == kStageGeneral) {
+    InsPre<D> P;
+    insert_prefetch<D>(P, st, in, h, n);
+    insert_phase<D>(S, st, in, h, P, n);
+    return;
+  }
+  if (status != kStageOne && status != kStageSplit) return;
+  const int row = stage_get(stg, 1), p = stage_get(stg, 2), new_end = stage_get(stg, 3);
+  const int cn = stage_get(stg, 4), n_act = stage_get(stg, 7), flags = stage_get(stg, 8);
+  const float mx = __int_as_float(stage_get(stg, 5)), mn = __int_as_float(stage_get(stg, 6));
+  if (tid < D / 4) reinterpret_cast<int*>(H.dir8 + (int64_t)row * D)[tid] = stage_get(stg, kStageHead + tid);
+  if (tid == 0) {
+    H.mmax[row] = mx;
+    H.mmin[row] = mn;
+    H.count[row] = cn;
+    H.labels[p] = (int16_t)row;
+    st.end[h] = new_end;
+    st.flags[h] = flags;
+  }
+  if (status == kStageSplit) {
+    if (tid < D) S.mu[tid] = st.mu_ref[(int64_t)h * D + tid];
+    __syncthreads();                                     // the label and summaries above are written
+    split_cluster(S, st, H, head_keys_of(st, in, h), h, row, n_act, p + 1);
+    if (tid == 0 && n_act + 1 >= in.reset_at) st.flags[h] = flags | 2;
+  }
 }
 
 }  // namespace ssa

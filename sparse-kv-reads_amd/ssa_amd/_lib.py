@@ -45,7 +45,10 @@ class IndexState(ct.Structure):
                 ("rbar", vp), ("cap", vp), ("vthr", vp),
                 ("flags", vp), ("end", vp), ("nsplit", vp),
                 ("labels", vp),
-                ("mem", vp), ("proj", vp), ("side", vp), ("smag", vp)]
+                ("mem", vp), ("proj", vp), ("side", vp), ("smag", vp),
+                ("stage", vp)]
+
+STAGE_WORDS = 80          # SSA_STAGE_WORDS
 
 
 class InsertArgs(ct.Structure):

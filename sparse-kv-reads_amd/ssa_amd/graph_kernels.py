@@ -26,7 +26,7 @@ from .labeled_attn import SplitWork, attn_args, default_splits
 from .sphere_fused import SphereIndexFused
 
 STACKED = ("n_c", "sum_dir", "dir8", "cent", "cent8", "mmax", "mmin", "count", "ksum", "mu_ref", "rbar", "flags",
-           "cap", "vthr", "_mem", "_proj", "_side", "_smag", "nsplit", "labels", "end_dev")
+           "cap", "vthr", "_mem", "_proj", "_side", "_smag", "_stage", "nsplit", "labels", "end_dev")
 
 
 class DenseAttentionGraph:

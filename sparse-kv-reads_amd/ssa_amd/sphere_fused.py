@@ -28,8 +28,8 @@ import math
 
 import torch
 
-from ._lib import (BuildArgs, IndexState, InsertArgs, SelectArgs, check, dtype_tag, lib, ptr, require_cuda,
-                   stream_ptr)
+from ._lib import (STAGE_WORDS, BuildArgs, IndexState, InsertArgs, SelectArgs, check, dtype_tag, lib, ptr,
+                   require_cuda, stream_ptr)
 from .labeled_attn import _work, attn_args, default_splits
 
 GROUPS = ("per_head", "max", "max_rel", "sum_share")
@@ -139,6 +139,7 @@ class SphereIndexFused:
         self._proj = torch.zeros(H_kv, self.MS, **f32)
         self._side = torch.zeros(H_kv, self.MS, dtype=torch.int32, device=device)
         self._smag = torch.zeros(H_kv, self.MS, **f32)
+        self._stage = torch.zeros(H_kv, STAGE_WORDS, dtype=torch.int32, device=device)
         self._flags_host = torch.zeros(H_kv, dtype=torch.int32, pin_memory=True)
         self._pending = None
         self._w = {}
@@ -162,6 +163,7 @@ class SphereIndexFused:
         s.ksum, s.mu_ref, s.rbar, s.cap, s.vthr = p("ksum"), p("mu_ref"), p("rbar"), p("cap"), p("vthr")
         s.flags, s.end, s.nsplit, s.labels = p("flags"), p("end_dev"), p("nsplit"), p("labels")
         s.mem, s.proj, s.side, s.smag = p("_mem"), p("_proj"), p("_side"), p("_smag")
+        s.stage = p("_stage")
         return s
 
     def _insert_args(self, K: torch.Tensor, *, n_host: int = 0, n_dev: torch.Tensor | None = None,
