@@ -150,7 +150,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane / LPR, li = lane % LPR;
-  const int sp = blockIdx.x, h = blockIdx.y;
+  // XCD-aware placement: workgroups are dispatched to the 8 XCDs round robin by linear id, so
+  // (when the head count allows) every workgroup of a head goes to the same XCD and the head's
+  // index state, labels and partials are shared through one L2. Any mapping is correct; this one
+  // is a permutation of the grid.
+  int sp = blockIdx.x, h = blockIdx.y;
+  if ((gridDim.y & 7) == 0) {
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int j = lin >> 3;
+    h = (lin & 7) + 8 * (j / gridDim.x);
+    sp = j % gridDim.x;
+  }
   const int G = a.G, S = a.S;
   const bool per_head = !DENSE && a.per_head;
 

@@ -551,11 +551,7 @@ __device__ __forceinline__ void insert_stage(SM& S, const ssa_index_state_t& st,
   }
   block_argmax(S, best, bi);
   const int row = bi;
-  if (tid < D) {
-    const float sd = H.sum_dir[(int64_t)row * D + tid] + S.kn[tid];
-    H.sum_dir[(int64_t)row * D + tid] = sd;       // the attention reads only the int8 copy
-    S.sd[tid] = sd;
-  }
+  if (tid < D) S.sd[tid] = H.sum_dir[(int64_t)row * D + tid] + S.kn[tid];
   if (row < kT && tid == row) { S.rmx = P.mx; S.rmn = P.mn; S.rcnt = P.cnt; }
   if (row >= kT && tid == 0) { S.rmx = H.mmax[row]; S.rmn = H.mmin[row]; S.rcnt = H.count[row]; }
   __syncthreads();
@@ -568,6 +564,7 @@ __device__ __forceinline__ void insert_stage(SM& S, const ssa_index_state_t& st,
       const bool wide = (1.0f - sdsq / (cnf * cnf) > P.vthr) && (cn >= in.var_min);
       const bool over = cnf > fmaxf(P.cap, in.capk * (float)p);
       const bool split = (over || wide) && n_act < C && cn >= 2 && cn <= H.ms;
+      S.scali[0] = split ? 1 : 0;
       stage_put(stg, 0, split ? kStageSplit : kStageOne);
       stage_put(stg, 1, row);
       stage_put(stg, 2, p);
@@ -579,6 +576,10 @@ __device__ __forceinline__ void insert_stage(SM& S, const ssa_index_state_t& st,
     }
   }
   __syncthreads();
+  // The fp32 direction sum is written now (the attention reads only the int8 copy) unless the
+  // cluster splits: the commit's split then rewrites it, and a write from here could reach
+  // memory after the split's (another XCD's L2 may write its line back later).
+  if (tid < D && !S.scali[0]) H.sum_dir[(int64_t)row * D + tid] = S.sd[tid];
   if (tid < D) S.d8[tid] = q8(S.sd[tid] / fmaxf(S.scal[1], 1e-12f));
   // running mean vs the centring mean: drift flag; cluster count: reset flag
   const float nb = (float)(new_end - 1);

@@ -227,34 +227,32 @@ __device__ __forceinline__ unsigned long long rank_key(float key, int c) {
 
 // Take cluster c iff it is live (cnt > 0) and the live clusters ranked before it, by (key desc,
 // index asc), hold fewer than `need` keys: before(c) < need.
-// Exact threshold search instead of a full ranking: bucket b(c) = top 10 bits of the rank key
-// is monotone in the rank order, so with b* the first bucket where the running key count
-// reaches need and base the count of all buckets before b*, every cluster of a bucket before b*
-// has before(c) <= base - cnt(c) < need (taken), every cluster of a bucket after b* has
-// before(c) >= base + count(b*) >= need (not taken), and a cluster of bucket b* has
-// before(c) = base + (its bucket's clusters ranked before it), counted exactly. If all keys
-// together are fewer than need, every live cluster is taken.
+// Exact threshold search instead of a full ranking. The bucket of a key,
+//   b(c) = min((desc_bits(key) - base) >> shift, kBins - 1)   (base <= desc_bits of every live key),
+// is monotone in the rank order. With b* the first bucket where the running key count reaches
+// need and cbase the count of all buckets before b*:
+//   - a cluster of a bucket before b* has before(c) <= cbase - cnt(c) < need (taken);
+//   - a cluster of a bucket after b* has before(c) >= cbase + count(b*) >= need (not taken);
+//   - a cluster of bucket b* has before(c) = cbase + (its bucket's clusters ranked before it),
+//     counted exactly.
+// If all keys together are fewer than need, every live cluster is taken.
 // On entry S.hist is zero and S.nlist is 0; both are so again on return.
 template <int NT, int KPT, int GMAX, typename Emit>
 __device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)[KPT], const int (&cnt)[KPT], int C,
-                                            int64_t need, int row, Emit emit) {
+                                            int64_t need, unsigned int base, int shift, int row, Emit emit) {
   static_assert(kBins == 4 * NT, "one int4 of buckets per thread");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  unsigned int db[KPT];
+  unsigned int db[KPT], bk[KPT];
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
     db[k] = desc_bits(key[k]);
-    if (cnt[k] > 0) atomicAdd(&S.hist[db[k] >> 22], cnt[k]);
+    bk[k] = min((db[k] > base ? db[k] - base : 0u) >> shift, (unsigned int)(kBins - 1));
+    if (cnt[k] > 0) atomicAdd(&S.hist[bk[k]], cnt[k]);
   }
   __syncthreads();
   const int4 hb = reinterpret_cast<const int4*>(S.hist)[tid];
   const int own = hb.x + hb.y + hb.z + hb.w;
-  int incl = own;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
-  }
+  const int incl = wave_incl_scan_dpp(own);
   if (lane == 63) S.wsum[wave] = incl;
   __syncthreads();
   int wbase = 0, total = 0;
@@ -281,10 +279,10 @@ __device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)
   reinterpret_cast<int4*>(S.hist)[tid] = make_int4(0, 0, 0, 0);     // this thread's buckets, read above
   __syncthreads();
   const unsigned int bstar = (unsigned int)S.bstar;
-  const int64_t base = S.base;
+  const int64_t cbase = S.base;
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    if (cnt[k] > 0 && (db[k] >> 22) == bstar) {
+    if (cnt[k] > 0 && bk[k] == bstar) {
       const int i = atomicAdd(&S.nlist, 1);
       S.lrk[i] = ((unsigned long long)db[k] << 32) | (unsigned int)(tid + k * NT);
       S.lcnt[i] = cnt[k];
@@ -298,13 +296,24 @@ __device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)
     if (c >= C) break;
     float x = 0.f;
     if (cnt[k] > 0) {
-      const unsigned int b = db[k] >> 22;
+      const unsigned int b = bk[k];
       if (b < bstar) {
         x = 1.f;
       } else if (b == bstar) {
         const unsigned long long rk = ((unsigned long long)db[k] << 32) | (unsigned int)c;
-        int64_t before = base;
-        for (int i = 0; i < nl; ++i) before += S.lrk[i] < rk ? S.lcnt[i] : 0;
+        int64_t before = cbase;
+        for (int i0 = 0; i0 < nl; i0 += 8) {
+          unsigned long long r8[8];
+          int n8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = min(i0 + e, nl - 1);
+            r8[e] = S.lrk[i];
+            n8[e] = S.lcnt[i];
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) before += (i0 + e < nl && r8[e] < rk) ? n8[e] : 0;
+        }
         x = before < need ? 1.f : 0.f;
       }
     }
@@ -381,7 +390,7 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
         for (int g2 = 0; g2 < GMAX; ++g2)
           if (g2 == g) key[k] = z[k][g2];
       }
-      bucket_take<NT, KPT>(S, key, cnt, C, need, g, emit);
+      bucket_take<NT, KPT>(S, key, cnt, C, need, 0u, 22, g, emit);
     }
     return;
   }
@@ -393,7 +402,7 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
       float v = -INFINITY;
 #pragma unroll
       for (int k = 0; k < KPT; ++k) v = fmaxf(v, z[k][g]);
-      v = wave_max(v);
+      v = wave_max_dpp(v);
       if (lane == 0 && g < G) S.red[g][wave] = v;
     }
     __syncthreads();
@@ -437,12 +446,15 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
       for (int half = kMaxC / 128; half >= 1; half >>= 1)
 #pragma unroll
         for (int k = 0; k < half; ++k) u[k] = u[k] + u[k + half];
+      // strides 32 and 16 by shuffles, 8 .. 1 by DPP row_shl (lane l reads lane l + h of its
+      // row); only lanes below the stride keep meaningful sums
       float v = u[0];
-#pragma unroll
-      for (int hh = 32; hh >= 1; hh >>= 1) {
-        const float o = __shfl_down(v, hh, 64);
-        if (lane < hh) v = v + o;
-      }
+      v = v + __shfl_down(v, 32, 64);
+      v = v + __shfl_down(v, 16, 64);
+      v = v + dpp_f<0x108, 0xF>(0.f, v);
+      v = v + dpp_f<0x104, 0xF>(0.f, v);
+      v = v + dpp_f<0x102, 0xF>(0.f, v);
+      v = v + dpp_f<0x101, 0xF>(0.f, v);
       if (lane == 0) S.tree[g] = v;
     }
     __syncthreads();
@@ -466,7 +478,9 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
     }
     __syncthreads();                          // S.hist / S.nlist cleared
   }
-  bucket_take<NT, KPT>(S, key, cnt, C, need, 0, emit);
+  // sum_share keys lie in [0, G] (each head's share is at most 1): 32 buckets per binade below G
+  if (group == 0) bucket_take<NT, KPT>(S, key, cnt, C, need, desc_bits((float)G), 18, 0, emit);
+  else bucket_take<NT, KPT>(S, key, cnt, C, need, 0u, 22, 0, emit);
 }
 
 }  // namespace ssa

@@ -111,6 +111,38 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// DPP forms of the wave reductions (row_shr within 16-lane rows, then row_bcast:15 and
+// row_bcast:31 across rows): a lane whose source is out of its row or in a disabled row takes
+// the `old` operand.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+// Maximum over the 64 lanes, returned to every lane (read from lane 63, which holds it).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f<0x111, 0xF>(v, v));      // row_shr:1
+  v = fmaxf(v, dpp_f<0x112, 0xF>(v, v));      // row_shr:2
+  v = fmaxf(v, dpp_f<0x114, 0xF>(v, v));      // row_shr:4
+  v = fmaxf(v, dpp_f<0x118, 0xF>(v, v));      // row_shr:8
+  v = fmaxf(v, dpp_f<0x142, 0xA>(v, v));      // row_bcast:15 into rows 1 and 3
+  v = fmaxf(v, dpp_f<0x143, 0xC>(v, v));      // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_incl_scan_dpp(int v) {
+  v += dpp_i<0x111, 0xF>(0, v);
+  v += dpp_i<0x112, 0xF>(0, v);
+  v += dpp_i<0x114, 0xF>(0, v);
+  v += dpp_i<0x118, 0xF>(0, v);
+  v += dpp_i<0x142, 0xA>(0, v);
+  v += dpp_i<0x143, 0xC>(0, v);
+  return v;
+}
+
 // (score, index) argmax with the lowest index winning ties; index -1 never wins.
 __device__ __forceinline__ void argmax_merge(float& s, int& i, float s2, int i2) {
   bool take = (i < 0) || (i2 >= 0 && (s2 > s || (s2 == s && i2 < i)));
