@@ -16,6 +16,8 @@
  *               _to8 / _refresh8      src/ssa/kernels/sphere_fused.py:394-405
  * Canonical order (the definition both sides implement):
  *   dot(a,b)   8 chains, chain j = fma over elements j, j+8, ...; ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7))
+ *   scoring dot (selection scores only): 8 chains, chain j = fma over elements j*d/8 .. (j+1)*d/8-1
+ *              in order, combined in the same tree
  *   unit(x)    x / max(sqrt(dot(x,x)), 1e-12)
  *   q8(u)      floor(u*127 + 0.5), multiply and add rounded separately
  *   exp(x<=0)  Cody-Waite by ln2 (hi 0.693145751953125, lo 1.42860682030941723e-6), degree-7
@@ -35,6 +37,18 @@ float canon_dot(const float* a, const float* b, int d) {
   float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int i = 0; i < d; i += 8)
     for (int j = 0; j < 8; ++j) c[j] = fmaf(a[i + j], b[i + j], c[j]);
+  return ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+}
+
+/* Scoring dot (the selection's scores): chain j sums elements [j*d/8, (j+1)*d/8) left to right
+ * with fma; the chains are combined as in canon_dot. */
+float canon_dot_chunked(const float* a, const float* b, int d) {
+  float c[8];
+  const int e = d / 8;
+  for (int j = 0; j < 8; ++j) {
+    c[j] = 0.f;
+    for (int k = 0; k < e; ++k) c[j] = fmaf(a[j * e + k], b[j * e + k], c[j]);
+  }
   return ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
 }
 
@@ -290,9 +304,9 @@ void canon_select(const canon_head_t* H, const float* q, int G, double budget, i
     if (!live) { for (int g = 0; g < G; ++g) z[(int64_t)g * C + c] = -INFINITY; continue; }
     for (int i = 0; i < d; ++i)
       dv[i] = (H->summary_bits == 8 && H->dir8) ? (float)H->dir8[(int64_t)c * d + i] : H->sum_dir[(int64_t)c * d + i];
-    const float nrm = fmaxf(sqrtf(canon_dot(dv, dv, d)), 1e-12f);
+    const float nrm = fmaxf(sqrtf(canon_dot_chunked(dv, dv, d)), 1e-12f);
     for (int g = 0; g < G; ++g) {
-      const float p = canon_dot(q + (int64_t)g * d, dv, d) / nrm;
+      const float p = canon_dot_chunked(q + (int64_t)g * d, dv, d) / nrm;
       const float e = p >= 0.f ? H->mmax[c] * p : H->mmin[c] * p;
       z[(int64_t)g * C + c] = group == 1 ? e : e * scale;
     }

@@ -39,6 +39,8 @@ def lib():
         _lib = ct.CDLL(str(LIB))
         _lib.canon_dot.restype = ct.c_float
         _lib.canon_dot.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int]
+        _lib.canon_dot_chunked.restype = ct.c_float
+        _lib.canon_dot_chunked.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int]
         _lib.canon_exp.restype = ct.c_float
         _lib.canon_exp.argtypes = [ct.c_float]
         _lib.canon_q8.restype = ct.c_int8
@@ -73,6 +75,13 @@ def canon_dot(a, b) -> float:
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)
     return float(lib().canon_dot(_p(a), _p(b), a.shape[0]))
+
+
+def canon_dot_chunked(a, b) -> float:
+    """The selection's scoring dot: chain j over elements [j*d/8, (j+1)*d/8)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return float(lib().canon_dot_chunked(_p(a), _p(b), a.shape[0]))
 
 
 def canon_exp(x: float) -> float:

@@ -192,24 +192,64 @@ struct SelSmem {
 // memory latency overlaps the query and label loads.
 template <int D>
 struct SelPre {
-  int4 raw[D / 16];                 // int8 direction row (8-bit summaries only)
-  int cnt;
+  int4 raw[D / 16];                 // int8 chunks of the first round's 8 rows (8-bit summaries only)
+  int cnt;                          // summaries of slot sel_slot(threadIdx.x, 0)
   float mx, mn;
 };
 
+// Scoring layout: 8 lanes score one cluster row together, lane j holding chain j (elements
+// [j*D/8, (j+1)*D/8)). Lane group grp = t / 8 scores, in round k, the rows grp + 256k + 32i
+// (i < 8), and afterwards thread t keeps the scores of slot grp + 256k + 32 * (t % 8).
+__device__ __forceinline__ int sel_slot(int t, int k) { return (t >> 3) + 256 * k + 32 * (t & 7); }
+
+// Lane j's int8 chunk of a row of D values: D/8 consecutive bytes.
+template <int D>
+__device__ __forceinline__ void load_chunk8(const int8_t* row, int j, int4* dst, int i) {
+  constexpr int E = D / 8;
+  const int8_t* p = row + j * E;
+  if constexpr (E >= 16) {
+#pragma unroll
+    for (int n = 0; n < E / 16; ++n) dst[i * (E / 16) + n] = reinterpret_cast<const int4*>(p)[n];
+  } else {
+    // E bytes of chunk i go to bytes [i*E, (i+1)*E) of dst (E = 2, 4 or 8)
+    int* w = reinterpret_cast<int*>(dst);
+    if constexpr (E == 8) {
+      const int2 v = *reinterpret_cast<const int2*>(p);
+      w[2 * i] = v.x; w[2 * i + 1] = v.y;
+    } else if constexpr (E == 4) {
+      w[i] = *reinterpret_cast<const int*>(p);
+    } else {
+      const int v = *reinterpret_cast<const unsigned short*>(p);
+      w[i / 2] = (i & 1) ? ((w[i / 2] & 0xffff) | (v << 16)) : v;
+    }
+  }
+}
+
 template <int D>
 __device__ __forceinline__ void sel_prefetch(SelPre<D>& P, const Head& H, int C) {
-  const int c = threadIdx.x;
+  const int t = threadIdx.x, j = t & 7, grp = t >> 3;
+  const int c = sel_slot(t, 0);
   P.cnt = 0; P.mx = 0.f; P.mn = 0.f;
   if (c < C) {
     P.cnt = H.count[c];
     P.mx = H.mmax[c];
     P.mn = H.mmin[c];
-    if (H.q8dirs) {
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) P.raw[k] = reinterpret_cast<const int4*>(H.dir8 + (int64_t)c * D)[k];
-    }
   }
+  if (H.q8dirs) {
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) P.raw[k] = make_int4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_chunk8<D>(H.dir8 + (int64_t)min(grp + 32 * i, C - 1) * D, j, P.raw, i);
+  }
+}
+
+// Sum of v over the 8 lanes of a lane group in the canonical tree ((c0+c1)+(c2+c3)) +
+// ((c4+c5)+(c6+c7)), lane j holding c_j; every lane of the group gets the total.
+__device__ __forceinline__ float group8_sum(float v) {
+  v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));   // lane ^ 1
+  v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));   // lane ^ 2
+  v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));  // 7 - lane
+  return v;
 }
 
 // Orderable bits of a key for the selection order: ascending bits = descending key; -0 and +0
@@ -284,7 +324,7 @@ __device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)
   for (int k = 0; k < KPT; ++k) {
     if (cnt[k] > 0 && bk[k] == bstar) {
       const int i = atomicAdd(&S.nlist, 1);
-      S.lrk[i] = ((unsigned long long)db[k] << 32) | (unsigned int)(tid + k * NT);
+      S.lrk[i] = ((unsigned long long)db[k] << 32) | (unsigned int)sel_slot(tid, k);
       S.lcnt[i] = cnt[k];
     }
   }
@@ -292,8 +332,8 @@ __device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)
   const int nl = S.nlist;
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    const int c = tid + k * NT;
-    if (c >= C) break;
+    const int c = sel_slot(tid, k);
+    if (c >= C) continue;
     float x = 0.f;
     if (cnt[k] > 0) {
       const unsigned int b = bk[k];
@@ -346,25 +386,81 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
   }
   reinterpret_cast<int4*>(S.hist)[tid] = make_int4(0, 0, 0, 0);
   if (tid == 0) S.nlist = 0;
-  // scores e[g] = (p >= 0 ? mmax : mmin) * p, p = q_g . dir / |dir|, scaled by 1/sqrt(d) unless per_head
+  // scores e[g] = (p >= 0 ? mmax : mmin) * p, p = q_g . dir / |dir|, scaled by 1/sqrt(d) unless
+  // per_head; the dots are scoring dots (score_dots), 8 lanes per row
   float z[KPT][GMAX];
   int cnt[KPT];
+  constexpr int E = D / 8;
+  constexpr bool QREG = E * GMAX <= 64;        // the lane's query slices fit in registers
+  const int jl = tid & 7, grp = tid >> 3;
+  float qv[QREG ? GMAX : 1][QREG ? E : 1];
+  if constexpr (QREG) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[g][e] = S.q[g][jl * E + e];
+  }
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    const int c = tid + k * NT;
+    if (256 * k >= C) {                         // no slot of this round exists (uniform)
+      cnt[k] = 0;
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) z[k][g] = -INFINITY;
+      continue;
+    }
+    float nrm2_i[8], dot_i[8][GMAX];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int cr = min(grp + 256 * k + 32 * i, C - 1);        // rows past C are never kept
+      float x[E];
+      if (H.q8dirs) {
+        int4 raw[(E + 15) / 16 + (E < 16 ? 1 : 0)];
+        const int8_t* bytes;
+        if (k == 0) {
+          bytes = reinterpret_cast<const int8_t*>(P.raw) + i * E;
+        } else {
+          load_chunk8<D>(H.dir8 + (int64_t)cr * D, jl, raw, 0);
+          bytes = reinterpret_cast<const int8_t*>(raw);
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = (float)bytes[e];
+      } else {
+        const float* rp = H.sum_dir + (int64_t)cr * D + jl * E;
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = rp[e];
+      }
+      float cn = 0.f, cq[GMAX];
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) cq[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        cn = __builtin_fmaf(x[e], x[e], cn);
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g)
+          cq[g] = __builtin_fmaf(QREG ? qv[QREG ? g : 0][QREG ? e : 0] : S.q[g][jl * E + e], x[e], cq[g]);
+      }
+      nrm2_i[i] = group8_sum(cn);
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) dot_i[i][g] = group8_sum(cq[g]);
+    }
+    // lane j keeps row i = j of the round
+    float nrm2 = nrm2_i[0], dot[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) dot[g] = dot_i[0][g];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+      nrm2 = jl == i ? nrm2_i[i] : nrm2;
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) dot[g] = jl == i ? dot_i[i][g] : dot[g];
+    }
+    const int c = sel_slot(tid, k);
     const bool used = c < C && c < n_act;
-    float mx = 0.f, mn = 0.f, nrm2 = 0.f, dot[GMAX];
+    float mx = 0.f, mn = 0.f;
     int ct = 0;
     if (k == 0) {
       ct = P.cnt; mx = P.mx; mn = P.mn;
-      if (used) {
-        if (H.q8dirs) row_dots_raw<D, GMAX>(P.raw, S.q, G, nrm2, dot);
-        else row_dots<D, GMAX>(H.sum_dir + (int64_t)c * D, S.q, G, nrm2, dot);
-      }
     } else if (used) {
       ct = H.count[c]; mx = H.mmax[c]; mn = H.mmin[c];
-      if (H.q8dirs) row_dots<D, GMAX>(H.dir8 + (int64_t)c * D, S.q, G, nrm2, dot);
-      else row_dots<D, GMAX>(H.sum_dir + (int64_t)c * D, S.q, G, nrm2, dot);
     }
     cnt[k] = used && ct > 0 ? ct : 0;
     const float nrm = fmaxf(sqrtf(nrm2), 1e-12f);
@@ -425,7 +521,7 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
     float t[KPT][GMAX];
 #pragma unroll
     for (int k = 0; k < KPT; ++k) {
-      const int c = tid + k * NT;
+      const int c = sel_slot(tid, k);
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
         t[k][g] = (cnt[k] > 0 && g < G) ? cexp(z[k][g] - zmx[g]) : 0.f;

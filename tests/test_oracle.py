@@ -54,6 +54,27 @@ def test_canonical_dot_matches_float64_and_is_exact_on_small_integers():
         assert canon_dot(ia, ib) == float(np.dot(ia.astype(np.int64), ib.astype(np.int64)))
 
 
+def test_scoring_dot_matches_float64_and_is_exact_on_small_integers():
+    from oracle.canon import canon_dot_chunked
+    g = np.random.default_rng(1)
+    for d in (16, 64, 128, 256):
+        a = g.standard_normal(d).astype(np.float32)
+        b = g.standard_normal(d).astype(np.float32)
+        err = abs(canon_dot_chunked(a, b) - float(np.dot(a.astype(np.float64), b.astype(np.float64))))
+        assert err <= 1e-6 * float(np.abs(a.astype(np.float64) * b).sum()) + 1e-30
+        ia = g.integers(-127, 128, d).astype(np.float32)
+        ib = g.integers(-127, 128, d).astype(np.float32)
+        assert canon_dot_chunked(ia, ib) == float(np.dot(ia.astype(np.int64), ib.astype(np.int64)))
+    # the chains are contiguous blocks: a value that cancels within a block vanishes exactly,
+    # while the interleaved order keeps the small term's rounding
+    d = 128
+    a = np.zeros(d, np.float32)
+    a[0], a[1], a[8] = 2.0 ** 30, 1.0, -(2.0 ** 30)       # one block; chains 0, 1, 0 when interleaved
+    b = np.ones(d, np.float32)
+    assert canon_dot_chunked(a, b) == 0.0                    # 2^30 + 1 rounds to 2^30, then - 2^30
+    assert canon_dot(a, b) == 1.0                            # chain 0: 2^30 - 2^30 = 0, chain 1: 1
+
+
 def test_q8_closed_values():
     assert canon_q8(1.0) == 127 and canon_q8(-1.0) == -127 and canon_q8(0.0) == 0
     assert canon_q8(0.5 / 127) == 1 and canon_q8(-0.5 / 127) == 0          # floor(u*127 + 0.5)
