@@ -172,6 +172,34 @@ typedef struct ssa_build_args {
  * src/ssa/kernels/sphere_fused.py:394-409). */
 int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b, void* stream);
 
+/* ---- division of over-cap clusters after a fit -------------------------------------------- */
+
+typedef struct ssa_split_args {
+  const void* k; int32_t k_dtype; int64_t s_kh; int64_t s_kn;   /* [Hk, capacity, d] */
+  const int32_t* heads; int32_t n_sel;   /* heads to divide */
+  int32_t start, end;                    /* binned range [start, end) */
+  float split_factor;
+  float cap_min;             /* cap_now = max(cap[h], cap_min) */
+  int32_t nmeans;            /* 1: k-means into max(2, ceil(count * split_factor / cap_now)) parts; 0: bisection */
+  int32_t iters;             /* k-means updates */
+  int32_t* mem; int32_t* side; float* proj; float* smag;   /* scratch [n_sel, ms] */
+  int32_t ms;                /* members held per cluster (at least the largest cluster) */
+  int32_t* over;             /* [n_sel] out: clusters over the cap at the start of the round */
+  int32_t* done;             /* [n_sel] out: clusters divided in the round (-1: more than 32 parts asked) */
+  int32_t refresh_only;      /* 1: only rebuild the int8 copies of the heads (after the last round) */
+} ssa_split_args_t;
+
+/* One round of the division of clusters over their cap after a k-means fit: the clusters with
+ * count > cap_now, in slot order over the heads in order, each divided into parts (k-means from
+ * members j*m/k, or the bisection of ssa_insert's split); non-empty parts are numbered in order,
+ * part 0 keeps the slot and the others take spare slots handed out in order within batches of
+ * 64 clusters. The caller repeats rounds (a k-means round, then bisection rounds) until no cluster
+ * is over its cap or a bisection round divides nothing, then refreshes the int8 copies.
+ * Replaces SphereIndexGPU._split_overflow / _split_batch / _kmeans_padded / _bisect_padded
+ * (src/ssa/attn/sphere_gpu.py:56-102,307-391) and SphereIndexFused._split_overflow
+ * (src/ssa/kernels/sphere_fused.py:411-413). */
+int ssa_split_fit(const ssa_index_state_t* st, const ssa_split_args_t* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

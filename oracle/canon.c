@@ -207,6 +207,132 @@ static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {
   free(mem); free(mag); free(proj); free(side); free(kr); free(kn); free(a); free(b); free(s0); free(s1); free(vs);
 }
 
+/* ---- division after a fit ------------------------------------------------------------------ */
+/* One round of SphereIndexGPU._split_overflow for one head (src/ssa/attn/sphere_gpu.py:307-391):
+ * the clusters over the cap (count > cap_now, slot < n_c, count >= 2) are taken in slot order;
+ * cluster i of the head has global rank rank0 + i in the round (heads in order), and spare
+ * slots are handed out within batches of 64 ranks: base starts each batch at n_c and grows by
+ * every cluster's new-part count, kept or not. nmeans: k = max(2, ceil(count * split_factor /
+ * cap_now)) parts by cosine k-means from the members at j*m/k (_kmeans_padded :56-73), iters
+ * updates then a final assignment (lowest part on ties); otherwise the bisection of the
+ * insertion's split (_bisect_padded :76-102). Non-empty parts are numbered in order; part 0 keeps
+ * the slot, part p > 0 takes base + p - 1; a cluster is split when all fit in C. Sums run over
+ * members in position order. The int8 copies are left to a refresh. Returns the clusters split;
+ * *n_over receives the number of clusters over the cap. */
+#define KMAX 32
+static void kmeans_parts(const float* K, int d, const float* mu, const int* mem, const float* mag, int m, int k,
+                         int iters, int* part) {
+  float* cent = (float*)malloc(sizeof(float) * (size_t)k * d);
+  float* sums = (float*)malloc(sizeof(float) * (size_t)k * d);
+  int* cnt = (int*)malloc(sizeof(int) * k);
+  float* kn = (float*)malloc(sizeof(float) * d);
+  for (int p = 0; p < k; ++p) {
+    int j = (int)(((int64_t)p * m) / k);
+    if (j > m - 1) j = m - 1;
+    kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), cent + (int64_t)p * d);
+  }
+  for (int it = 0; it <= iters; ++it) {
+    for (int j = 0; j < m; ++j) {
+      kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
+      int best = 0;
+      float bs = canon_dot(kn, cent, d);
+      for (int p = 1; p < k; ++p) {
+        float sc = canon_dot(kn, cent + (int64_t)p * d, d);
+        if (sc > bs) { bs = sc; best = p; }
+      }
+      part[j] = best;
+    }
+    if (it == iters) break;
+    for (int p = 0; p < k; ++p) { cnt[p] = 0; for (int i = 0; i < d; ++i) sums[(int64_t)p * d + i] = 0.f; }
+    for (int j = 0; j < m; ++j) {
+      kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
+      float* sp = sums + (int64_t)part[j] * d;
+      for (int i = 0; i < d; ++i) sp[i] = sp[i] + kn[i];
+      cnt[part[j]] += 1;
+    }
+    for (int p = 0; p < k; ++p)
+      if (cnt[p] > 0) unit(sums + (int64_t)p * d, cent + (int64_t)p * d, d);
+  }
+  free(cent); free(sums); free(cnt); free(kn);
+}
+
+int canon_split_fit_head(canon_head_t* H, const float* K, int start, int end, float split_factor, float cap_now,
+                         int nmeans, int iters, int rank0, int* n_over) {
+  const int C = H->C, d = H->d;
+  int* list = (int*)malloc(sizeof(int) * C);
+  int no = 0;
+  for (int c = 0; c < *H->n_c && c < C; ++c)
+    if ((float)H->count[c] > cap_now && H->count[c] >= 2) list[no++] = c;
+  *n_over = no;
+  int n_cur = *H->n_c, base = n_cur, done = 0;
+  int* mem = (int*)malloc(sizeof(int) * (size_t)(end > 0 ? end : 1));
+  int* part = (int*)malloc(sizeof(int) * (size_t)(end > 0 ? end : 1));
+  float* mag = (float*)malloc(sizeof(float) * (size_t)(end > 0 ? end : 1));
+  float* kr = (float*)malloc(sizeof(float) * d);
+  float* kn = (float*)malloc(sizeof(float) * d);
+  float* sums = (float*)malloc(sizeof(float) * (size_t)KMAX * d);
+  for (int i = 0; i < no; ++i) {
+    const int c = list[i];
+    if ((rank0 + i) % 64 == 0) base = n_cur;
+    if (!nmeans) {
+      /* bisection: the insertion's split, into slot base when it fits */
+      if (base + 1 <= C) {
+        split(H, K, c, base, end);
+        if (*H->n_c == base + 1) { n_cur = base + 1; ++done; }
+      }
+      base += 1;
+      continue;
+    }
+    int m = 0;
+    for (int j = start; j < end; ++j)
+      if (H->labels[j] == c) mem[m++] = j;
+    for (int j = 0; j < m; ++j) {
+      for (int t = 0; t < d; ++t) kr[t] = K[(int64_t)mem[j] * d + t] - H->mu_ref[t];
+      mag[j] = sqrtf(canon_dot(kr, kr, d));
+    }
+    const float kf = ceilf(((float)m * split_factor) / cap_now);
+    int k = kf < 2.f ? 2 : (int)kf;
+    if (k > KMAX) k = KMAX;
+    kmeans_parts(K, d, H->mu_ref, mem, mag, m, k, iters, part);
+    int sizes[KMAX], renum[KMAX], nz = 0;
+    for (int p = 0; p < k; ++p) sizes[p] = 0;
+    for (int j = 0; j < m; ++j) sizes[part[j]] += 1;
+    for (int p = 0; p < k; ++p) renum[p] = sizes[p] > 0 ? nz++ : -1;
+    const int extra = nz - 1;
+    if (extra > 0 && base + extra <= C) {
+      int slot[KMAX];
+      for (int p = 0; p < nz; ++p) slot[p] = p == 0 ? c : base + p - 1;
+      for (int p = 0; p < nz; ++p) {
+        const int s = slot[p];
+        for (int t = 0; t < d; ++t) sums[(int64_t)p * d + t] = 0.f;
+        H->mmax[s] = 0.f; H->mmin[s] = INFINITY; H->count[s] = 0;
+      }
+      for (int j = 0; j < m; ++j) {
+        const int p = renum[part[j]], s = slot[p];
+        kn_of(K, d, H->mu_ref, mem[j], fmaxf(mag[j], 1e-12f), kn);
+        float* sp = sums + (int64_t)p * d;
+        for (int t = 0; t < d; ++t) sp[t] = sp[t] + kn[t];
+        H->mmax[s] = fmaxf(H->mmax[s], mag[j]);
+        H->mmin[s] = fminf(H->mmin[s], mag[j]);
+        H->count[s] += 1;
+        H->labels[mem[j]] = (int16_t)s;
+      }
+      for (int p = 0; p < nz; ++p) {
+        const int s = slot[p];
+        memcpy(H->sum_dir + (int64_t)s * d, sums + (int64_t)p * d, sizeof(float) * d);
+        unit(sums + (int64_t)p * d, H->cent + (int64_t)s * d, d);
+      }
+      n_cur += extra;
+      *H->n_c = n_cur;
+      *H->nsplit += extra;
+      ++done;
+    }
+    base += extra > 0 ? extra : 0;
+  }
+  free(list); free(mem); free(part); free(mag); free(kr); free(kn); free(sums);
+  return done;
+}
+
 /* ---- insertion ---------------------------------------------------------------------------- */
 
 /* K: this head's keys widened to fp32, [capacity, d]. */
@@ -383,6 +509,16 @@ static void blocked_sums(const float* xn, int nb, int d, const int* as, int ncl,
 
 /* (Re)build one head from K[start:end) (fp32 [capacity, d]). mu: centring mean or NULL.
  * fit: k-means with C_fit clusters from init_idx (offsets into the range) first. */
+/* int8 copies of every slot: dir8 = q8(unit(sum_dir)), cent8 = q8(unit(cent)) (_refresh8,
+ * src/ssa/kernels/sphere_fused.py:398-405). */
+void canon_refresh8(canon_head_t* H) {
+  const int C = H->C, d = H->d;
+  for (int c = 0; c < C; ++c) {
+    if (H->dir8) q8_unit(H->sum_dir + (int64_t)c * d, H->dir8 + (int64_t)c * d, d);
+    if (H->cent8 && !H->shared_dirs) q8_unit(H->cent + (int64_t)c * d, H->cent8 + (int64_t)c * d, d);
+  }
+}
+
 void canon_build(canon_head_t* H, const float* K, int start, int end, const float* mu, int fit, int C_fit, int iters,
                  const int32_t* init_idx) {
   const int d = H->d, C = H->C, nb = end - start;
@@ -433,8 +569,5 @@ void canon_build(canon_head_t* H, const float* K, int start, int end, const floa
     }
     free(xn); free(mag); free(kr); free(as);
   }
-  for (int c = 0; c < C; ++c) {
-    if (H->dir8) q8_unit(H->sum_dir + (int64_t)c * d, H->dir8 + (int64_t)c * d, d);
-    if (H->cent8 && !H->shared_dirs) q8_unit(H->cent + (int64_t)c * d, H->cent8 + (int64_t)c * d, d);
-  }
+  canon_refresh8(H);
 }

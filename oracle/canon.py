@@ -51,6 +51,11 @@ def lib():
         _lib.canon_select.restype = None
         _lib.canon_select.argtypes = [ct.POINTER(HeadC), ct.c_void_p, ct.c_int, ct.c_double, ct.c_int, ct.c_float,
                                       ct.c_void_p]
+        _lib.canon_split_fit_head.restype = ct.c_int
+        _lib.canon_split_fit_head.argtypes = [ct.POINTER(HeadC), ct.c_void_p, ct.c_int, ct.c_int, ct.c_float,
+                                              ct.c_float, ct.c_int, ct.c_int, ct.c_int, ct.POINTER(ct.c_int)]
+        _lib.canon_refresh8.restype = None
+        _lib.canon_refresh8.argtypes = [ct.POINTER(HeadC)]
         _lib.canon_build.restype = None
         _lib.canon_build.argtypes = [ct.POINTER(HeadC), ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int,
                                      ct.c_int, ct.c_int, ct.c_void_p]
@@ -173,6 +178,32 @@ class CanonIndex:
             m = None if mu is None else np.ascontiguousarray(mu[i], dtype=np.float32)
             kh = np.ascontiguousarray(Kf[h])
             lib().canon_build(self._head(h), _p(kh), start, end, _p(m), int(fit), self.C_init, iters, _p(init))
+
+    def split_after_fit(self, K, *, start: int, end: int, split_factor: float, capk: float = 0.0,
+                        iters: int = 10, heads=None) -> int:
+        """Divide the clusters over their cap after a fit, in rounds (src/ssa/attn/sphere_gpu.py:
+        307-338): a k-means round, then bisection rounds until no cluster is over the cap or a round
+        divides nothing; then the int8 copies. Returns the number of rounds."""
+        Kf = self._keys(K)
+        heads = list(range(self.H_kv)) if heads is None else list(heads)
+        nmeans, rounds = True, 0
+        while True:
+            rank = over = done = 0
+            for h in heads:
+                cap_now = max(float(self.cap[h]), float(np.float32(capk * (end - start))))   # float32 clamp
+                n_over = ct.c_int(0)
+                kh = np.ascontiguousarray(Kf[h])
+                done += lib().canon_split_fit_head(self._head(h), _p(kh), start, end, float(split_factor),
+                                                   float(cap_now), int(nmeans), iters, rank, ct.byref(n_over))
+                rank += n_over.value
+                over += n_over.value
+            rounds += 1
+            if over == 0 or (done == 0 and not nmeans):
+                break
+            nmeans = False
+        for h in heads:
+            lib().canon_refresh8(self._head(h))
+        return rounds
 
     def insert(self, K, n: int, *, window: int = 64, delta: float = 0.03, capk: float = 0.0, reset_at: int = 0,
                var_min: int = 8) -> None:

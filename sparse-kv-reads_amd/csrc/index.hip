@@ -317,6 +317,223 @@ __global__ __launch_bounds__(kT) void refresh8_kernel(BuildArgs A) {
   }
 }
 
+// ---- division of over-cap clusters after a fit ------------------------------------------------
+//
+// Reference: SphereIndexGPU._split_overflow / _split_batch (src/ssa/attn/sphere_gpu.py:307-391)
+// with _kmeans_padded (:56-73) for the first round and _bisect_padded (:76-102) after it. One
+// workgroup per head takes that head's clusters over the cap in slot order, one at a time, so
+// the spare slots are handed out in the reference's order.
+
+constexpr int kKmax = 32;     // parts of one k-means division
+
+struct FitArgs {
+  ssa_index_state_t st;
+  ssa_split_args_t a;
+};
+
+struct FitSmem : InsertBase {
+  float cent[kKmax][kMaxD];
+  float sums[kKmax][kMaxD];
+  float pmx[kKmax], pmn[kKmax];
+  int cntp[kKmax], renum[kKmax], slot[kKmax];
+  int list[kMaxC];
+  int nlist, nz, bad;
+  union {
+    SplitTile spl;
+  } u;
+};
+
+__device__ __forceinline__ float fit_cap(const FitArgs& A, int h) { return fmaxf(A.st.cap[h], A.a.cap_min); }
+
+__device__ __forceinline__ bool fit_over(const FitArgs& A, int h, int c, float cap) {
+  const int ct = A.st.count[(int64_t)h * A.st.C + c];
+  return (float)ct > cap && ct >= 2;
+}
+
+// Clusters over the cap per head.
+__global__ __launch_bounds__(kT) void fit_count_kernel(FitArgs A) {
+  __shared__ int red[kW];
+  const int s = blockIdx.x, h = A.a.heads[s];
+  const float cap = fit_cap(A, h);
+  const int n_act = min(A.st.n_c[h], A.st.C);
+  int n = 0;
+  for (int c = threadIdx.x; c < n_act; c += kT) n += fit_over(A, h, c, cap) ? 1 : 0;
+  n = wave_sum_i(n);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = n;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int t = 0;
+    for (int w = 0; w < kW; ++w) t += red[w];
+    A.a.over[s] = t;
+  }
+}
+
+// S.sums[p] = ordered sum (members in position order) of the unit directions of the members in
+// part p (H.side), S.cntp[p] their number, for p < k.
+__device__ void fit_sums(FitSmem& S, const Head& H, const Keys& K, int m, int k) {
+  const int tid = threadIdx.x, d = H.d;
+  for (int e = tid; e < k * d; e += kT) S.sums[e / d][e % d] = 0.f;
+  if (tid < k) S.cntp[tid] = 0;
+  __syncthreads();
+  for (int t0 = 0; t0 < m; t0 += kTile) {
+    const int nr = min(kTile, m - t0);
+    for (int e = tid; e < nr * d; e += kT) {
+      const int r = e / d, i = e % d, j = t0 + r;
+      S.u.spl.tile[r][i] = (K(H.mem[j], i) - S.mu[i]) / fmaxf(H.smag[j], 1e-12f);
+    }
+    if (tid < nr) S.u.spl.tside[tid] = H.side[t0 + tid];
+    __syncthreads();
+    if (tid < d)
+      for (int r = 0; r < nr; ++r) {
+        const int p = S.u.spl.tside[r];
+        S.sums[p][tid] = S.sums[p][tid] + S.u.spl.tile[r][tid];
+      }
+    if (tid == kT - 1)
+      for (int r = 0; r < nr; ++r) S.cntp[S.u.spl.tside[r]] += 1;
+    __syncthreads();
+  }
+}
+
+// Cosine k-means of the m members into k parts (_kmeans_padded): centroids start at members
+// j*m/k, `iters` updates (a part with members takes the unit of its ordered sum), then a final
+// assignment; each member's part (the best canonical dot, lowest part on ties) goes to H.side.
+__device__ void fit_kmeans(FitSmem& S, const Head& H, const Keys& K, int m, int k, int iters) {
+  const int tid = threadIdx.x, d = H.d;
+  for (int e = tid; e < k * d; e += kT) {
+    const int p = e / d, i = e % d;
+    const int j = min((int)(((int64_t)p * m) / k), m - 1);
+    S.cent[p][i] = (K(H.mem[j], i) - S.mu[i]) / fmaxf(H.smag[j], 1e-12f);
+  }
+  __syncthreads();
+  for (int it = 0; it <= iters; ++it) {
+    for (int j = tid; j < m; j += kT) {
+      const int pos = H.mem[j];
+      const float magc = fmaxf(H.smag[j], 1e-12f);
+      auto kn = [&](int i) { return (K(pos, i) - S.mu[i]) / magc; };
+      int best = 0;
+      float bs = cdot_rolled(kn, [&](int i) { return S.cent[0][i]; }, d);
+      for (int p = 1; p < k; ++p) {
+        const float sc = cdot_rolled(kn, [&](int i) { return S.cent[p][i]; }, d);
+        if (sc > bs) { bs = sc; best = p; }
+      }
+      H.side[j] = best;
+    }
+    __syncthreads();
+    if (it == iters) break;
+    fit_sums(S, H, K, m, k);
+    for (int p = 0; p < k; ++p)
+      if (S.cntp[p] > 0) block_unit(S, S.sums[p], S.cent[p], d);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
+  __shared__ FitSmem S;
+  const ssa_index_state_t& st = A.st;
+  const ssa_split_args_t& a = A.a;
+  const int s = blockIdx.x, h = a.heads[s], tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, C = st.C;
+  const float cap = fit_cap(A, h);
+  // global rank of this head's first cluster over the cap: heads are taken in order
+  int r0 = 0;
+  for (int t = tid; t < s; t += kT) r0 += a.over[t];
+  r0 = block_sum_i(S, r0);
+  const int n_act0 = min(st.n_c[h], C);
+  if (tid == 0) { S.nlist = 0; S.bad = 0; }
+  __syncthreads();
+  for (int c0 = 0; c0 < n_act0; c0 += kT) {
+    const int c = c0 + tid;
+    const bool hit = c < n_act0 && fit_over(A, h, c, cap);
+    const int incl = wave_prefix_count(hit, lane);
+    if (lane == 63) S.red_i[wave] = incl;
+    __syncthreads();
+    int wb = 0, tot = 0;
+    for (int w2 = 0; w2 < kW; ++w2) { if (w2 < wave) wb += S.red_i[w2]; tot += S.red_i[w2]; }
+    if (hit) S.list[S.nlist + wb + incl - 1] = c;
+    __syncthreads();
+    if (tid == 0) S.nlist += tot;
+    __syncthreads();
+  }
+  Head H = head_view(st, h);
+  H.mem = a.mem + (int64_t)s * a.ms;
+  H.side = a.side + (int64_t)s * a.ms;
+  H.proj = a.proj + (int64_t)s * a.ms;
+  H.smag = a.smag + (int64_t)s * a.ms;
+  H.ms = a.ms;
+  Keys K;
+  K.dt = a.k_dtype;
+  K.s_kn = a.s_kn;
+  K.base = reinterpret_cast<const char*>(a.k) + (int64_t)elem_size(a.k_dtype) * (int64_t)h * a.s_kh;
+  if (tid < D) S.mu[tid] = st.mu_ref[(int64_t)h * D + tid];
+  __syncthreads();
+  const int nlist = S.nlist;
+  int n_cur = n_act0, base = n_act0, done = 0;
+  for (int i = 0; i < nlist; ++i) {
+    const int c = S.list[i];
+    if ((r0 + i) % 64 == 0) base = n_cur;                 // a new batch of 64
+    if (!a.nmeans) {
+      if (base + 1 <= C) {
+        split_cluster(S, st, H, K, h, c, base, a.end);
+        if (st.n_c[h] == base + 1) { n_cur = base + 1; ++done; }
+      }
+      base += 1;
+      continue;
+    }
+    const int m = gather_members(S, H, c, a.start, a.end);
+    for (int j = tid; j < m; j += kT) {
+      const int pos = H.mem[j];
+      auto kr = [&](int t) { return K(pos, t) - S.mu[t]; };
+      H.smag[j] = sqrtf(cdot_rolled(kr, kr, D));
+    }
+    __syncthreads();
+    const float kf = ceilf(((float)m * a.split_factor) / cap);
+    int k = kf < 2.f ? 2 : (int)kf;
+    if (k > kKmax) {
+      k = kKmax;
+      if (tid == 0) S.bad = 1;
+    }
+    fit_kmeans(S, H, K, m, k, a.iters);
+    fit_sums(S, H, K, m, k);                              // final parts: ordered sums and sizes
+    if (tid == 0) {
+      int nz = 0;
+      for (int p = 0; p < k; ++p) S.renum[p] = S.cntp[p] > 0 ? nz++ : -1;
+      for (int q = 0; q < nz; ++q) S.slot[q] = q == 0 ? c : base + q - 1;
+      S.nz = nz;
+      for (int q = 0; q < nz; ++q) { S.pmx[q] = 0.f; S.pmn[q] = INFINITY; }
+      for (int j = 0; j < m; ++j) {
+        const int q = S.renum[H.side[j]];
+        S.pmx[q] = fmaxf(S.pmx[q], H.smag[j]);
+        S.pmn[q] = fminf(S.pmn[q], H.smag[j]);
+      }
+    }
+    __syncthreads();
+    const int extra = S.nz - 1;
+    if (extra > 0 && base + extra <= C) {
+      for (int p = 0; p < k; ++p) {
+        const int q = S.renum[p];
+        if (q < 0) continue;
+        const int row = S.slot[q];
+        if (tid < D) H.sum_dir[(int64_t)row * D + tid] = S.sums[p][tid];
+        block_unit(S, S.sums[p], H.cent + (int64_t)row * D, D);
+        if (tid == 0) {
+          H.mmax[row] = S.pmx[q];
+          H.mmin[row] = S.pmn[q];
+          H.count[row] = S.cntp[p];
+        }
+      }
+      for (int j = tid; j < m; j += kT) H.labels[H.mem[j]] = (int16_t)S.slot[S.renum[H.side[j]]];
+      n_cur += extra;
+      if (tid == 0) {
+        st.n_c[h] = n_cur;
+        st.nsplit[h] = st.nsplit[h] + extra;
+      }
+      ++done;
+    }
+    base += extra > 0 ? extra : 0;
+    __syncthreads();
+  }
+  if (tid == 0) a.done[s] = S.bad ? -1 : done;
+}
+
 }  // namespace ssa
 
 // ---------------------------------------------------------------------------------------------
@@ -354,6 +571,35 @@ int launch_index(const IndexArgs& A, hipStream_t s) {
 }
 
 }  // namespace
+
+extern "C" int ssa_split_fit(const ssa_index_state_t* st, const ssa_split_args_t* a, void* stream) {
+  if (!state_ok(st) || !a || a->n_sel < 1 || !a->heads) return hipErrorInvalidValue;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a->refresh_only) {
+    BuildArgs B{};
+    B.st = *st;
+    B.b.heads = a->heads;
+    B.b.n_sel = a->n_sel;
+    if (st->dir8 || st->cent8) hipLaunchKernelGGL(refresh8_kernel, dim3(st->C, a->n_sel), dim3(kT), 0, s, B);
+    return hipGetLastError();
+  }
+  if (!a->k || !a->mem || !a->side || !a->proj || !a->smag || !a->over || !a->done || a->ms < 1 || a->start < 1 ||
+      a->end > st->capacity || a->iters < 0)
+    return hipErrorInvalidValue;
+  FitArgs A{};
+  A.st = *st;
+  A.a = *a;
+  hipLaunchKernelGGL(fit_count_kernel, dim3(a->n_sel), dim3(kT), 0, s, A);
+  switch (st->d) {
+    case 16: hipLaunchKernelGGL(fit_split_kernel<16>, dim3(a->n_sel), dim3(kT), 0, s, A); break;
+    case 32: hipLaunchKernelGGL(fit_split_kernel<32>, dim3(a->n_sel), dim3(kT), 0, s, A); break;
+    case 64: hipLaunchKernelGGL(fit_split_kernel<64>, dim3(a->n_sel), dim3(kT), 0, s, A); break;
+    case 128: hipLaunchKernelGGL(fit_split_kernel<128>, dim3(a->n_sel), dim3(kT), 0, s, A); break;
+    case 256: hipLaunchKernelGGL(fit_split_kernel<256>, dim3(a->n_sel), dim3(kT), 0, s, A); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 extern "C" int ssa_insert(const ssa_index_state_t* st, const ssa_insert_args_t* ins, void* stream) {
   if (!state_ok(st) || !ins) return hipErrorInvalidValue;

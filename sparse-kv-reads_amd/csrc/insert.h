@@ -191,17 +191,14 @@ __device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K,
   return block_sum_i(S, n1);
 }
 
-// Inlined (a call would put the caller's arguments and frame in scratch, whose set-up costs
-// every launch of the kernel); its dot loops stay rolled to keep registers down.
+// Positions of cluster c among [lo, hi), ascending, into H.mem[0 .. m) (at most H.ms); returns m.
 template <class SM>
-__device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st, const Head& H, const Keys& K, int h,
-                              int c, int nw, int stop) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = H.d;
-  // 1. members in ascending position order
+__device__ __forceinline__ int gather_members(SM& S, const Head& H, int c, int lo, int hi) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int m = 0;
-  for (int j0 = 1; j0 < stop; j0 += kT) {
+  for (int j0 = lo; j0 < hi; j0 += kT) {
     const int j = j0 + tid;
-    const bool hit = j < stop && H.labels[j] == c;
+    const bool hit = j < hi && H.labels[j] == c;
     const int incl = wave_prefix_count(hit, lane);
     if (lane == 63) S.red_i[wave] = incl;
     __syncthreads();
@@ -212,7 +209,17 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
     m += tot;
     __syncthreads();
   }
-  m = min(m, H.ms);
+  return min(m, H.ms);
+}
+
+// Inlined (a call would put the caller's arguments and frame in scratch, whose set-up costs
+// every launch of the kernel); its dot loops stay rolled to keep registers down.
+template <class SM>
+__device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st, const Head& H, const Keys& K, int h,
+                              int c, int nw, int stop) {
+  const int tid = threadIdx.x, d = H.d;
+  // 1. members in ascending position order
+  const int m = gather_members(S, H, c, 1, stop);
   if (m < 2) return;   // labels and counts disagree: leave the cluster as it is
   // 2. lengths
   for (int j = tid; j < m; j += kT) {

@@ -82,6 +82,18 @@ class BuildArgs(ct.Structure):
                 ("C_fit", i32), ("iters", i32)]
 
 
+class SplitArgs(ct.Structure):
+    _fields_ = [("k", vp), ("k_dtype", i32), ("s_kh", i64), ("s_kn", i64),
+                ("heads", vp), ("n_sel", i32),
+                ("start", i32), ("end", i32),
+                ("split_factor", f32), ("cap_min", f32),
+                ("nmeans", i32), ("iters", i32),
+                ("mem", vp), ("side", vp), ("proj", vp), ("smag", vp),
+                ("ms", i32),
+                ("over", vp), ("done", vp),
+                ("refresh_only", i32)]
+
+
 # (name, restype, argtypes) of every exported entry point; the C-ABI test checks this list
 # against the header.
 ENTRY_POINTS = {
@@ -95,6 +107,7 @@ ENTRY_POINTS = {
     "ssa_insert": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(InsertArgs), vp]),
     "ssa_select": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(InsertArgs), ct.POINTER(SelectArgs), vp]),
     "ssa_build": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(BuildArgs), vp]),
+    "ssa_split_fit": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SplitArgs), vp]),
     "ssa_sparse_step": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs),
                                    ct.POINTER(InsertArgs), vp]),
 }

@@ -28,8 +28,8 @@ import math
 
 import torch
 
-from ._lib import (STAGE_WORDS, BuildArgs, IndexState, InsertArgs, SelectArgs, check, dtype_tag, lib, ptr,
-                   require_cuda, stream_ptr)
+from ._lib import (STAGE_WORDS, BuildArgs, IndexState, InsertArgs, SelectArgs, SplitArgs, check, dtype_tag, lib,
+                   ptr, require_cuda, stream_ptr)
 from .labeled_attn import _work, attn_args, default_splits
 
 GROUPS = ("per_head", "max", "max_rel", "sum_share")
@@ -257,13 +257,42 @@ class SphereIndexFused:
             self._split_overflow(K, None, nmeans=True)
 
     def _split_overflow(self, K, cand=None, nmeans: bool = False) -> None:
-        """Division of over-cap clusters right after a fit (src/ssa/attn/sphere_gpu.py:302-391)."""
+        """Division of the clusters over their cap right after a fit, in rounds of ``ssa_split_fit``
+        (src/ssa/attn/sphere_gpu.py:307-338; src/ssa/kernels/sphere_fused.py:411-413): a k-means
+        round, then bisection rounds until no cluster is over its cap or a round divides nothing;
+        then the int8 copies. One host synchronisation per round, as in the reference."""
         if not self.splitting:
             return
-        over = (self.count.float() > self.cap.unsqueeze(1)) & (self.count >= 2)
-        if bool(over.any()):
-            raise NotImplementedError("post-fit division of over-cap clusters (split_factor > 0 at the fit) "
-                                      "is not implemented yet; later keys are split inside the insertion kernel")
+        H_kv, dev = self.H_kv, self.device
+        heads = torch.arange(H_kv, dtype=torch.int32, device=dev)
+        ms = max(int(self.count.max()), 2)                            # host sync
+        i32 = dict(dtype=torch.int32, device=dev)
+        mem, side = torch.empty(H_kv, ms, **i32), torch.empty(H_kv, ms, **i32)
+        proj = torch.empty(H_kv, ms, dtype=torch.float32, device=dev)
+        smag = torch.empty_like(proj)
+        over, done = torch.zeros(H_kv, **i32), torch.zeros(H_kv, **i32)
+        a = SplitArgs()
+        a.k, a.k_dtype, a.s_kh, a.s_kn = K.data_ptr(), dtype_tag(K.dtype), K.stride(0), K.stride(1)
+        a.heads, a.n_sel = heads.data_ptr(), H_kv
+        a.start, a.end = self.start, self.end
+        a.split_factor = self.split_factor
+        a.cap_min = float(torch.tensor(self.capk * (self.end - self.start), dtype=torch.float32))
+        a.iters = self.kmeans_iters
+        a.mem, a.side, a.proj, a.smag, a.ms = mem.data_ptr(), side.data_ptr(), proj.data_ptr(), smag.data_ptr(), ms
+        a.over, a.done = over.data_ptr(), done.data_ptr()
+        st = self._state()
+        nmeans = True
+        while True:
+            a.nmeans, a.refresh_only = int(nmeans), 0
+            check(lib().ssa_split_fit(st, a, stream_ptr(dev)), "ssa_split_fit")
+            n_over, n_done = int(over.sum()), done.cpu()                  # host sync
+            if bool((n_done < 0).any()):
+                raise RuntimeError("a cluster would be divided into more than 32 parts by the post-fit k-means")
+            if n_over == 0 or (int(n_done.sum()) == 0 and not nmeans):
+                break
+            nmeans = False
+        a.refresh_only = 1
+        check(lib().ssa_split_fit(st, a, stream_ptr(dev)), "ssa_split_fit")
 
     # -- decode ------------------------------------------------------------------------------
     def observe(self, K: torch.Tensor, n: int) -> None:

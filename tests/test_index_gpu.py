@@ -136,6 +136,33 @@ def test_in_kernel_splits_are_bit_exact_and_keep_the_cap():
     assert np.all(canon.count[np.arange(128)[None, :] >= canon.n_c[:, None]] == 0)
 
 
+@pytest.mark.parametrize("summary_bits", [8, 32])
+def test_post_fit_division_is_bit_exact(summary_bits):
+    """split_factor > 0 at the fit: the k-means round then the bisection rounds of the post-fit
+    division (src/ssa/attn/sphere_gpu.py:307-391) leave the same state on the GPU as in the
+    oracle, every cluster under the cap, and the following insertions and selection agree too."""
+    K, V, q = _keys(3, 2400, H=6, seed=9, centers=6)
+    n = 2000
+    idx = _fused(C=128, C_init=16, split_factor=2.0, summary_bits=summary_bits)
+    idx.observe(K, n)
+    canon = _canon_like(idx, K, n)
+    end = n - idx.window
+    canon.cap[:] = np.float32(2.0 * (end - 1) / 16)
+    rounds = canon.split_after_fit(K, start=1, end=end, split_factor=2.0, iters=idx.kmeans_iters)
+    _same(idx, canon)
+    assert rounds >= 2 and int(canon.nsplit.sum()) > 0 and idx.splits == int(canon.nsplit.sum())
+    for h in range(3):
+        nc = int(canon.n_c[h])
+        assert np.all(canon.count[h, :nc] <= canon.cap[h]) or nc == 128
+        assert np.array_equal(np.bincount(canon.labels[h, 1:end], minlength=128), canon.count[h])
+    for m in range(n + 1, n + 40):
+        idx.observe(K, m)
+        canon.insert(K, m, window=16, delta=math.inf)
+    _same(idx, canon)
+    w = idx.labels_and_weights(q, n=n + 39, budget=0.2)[1]
+    assert np.array_equal(w.cpu().numpy(), canon.select(q, budget=0.2))
+
+
 def test_end_to_end_config0_step():
     """Config 0: fp32, 16 query / 8 KV heads, d=128, n=4096, 256 clusters, 10 k-means iterations,
     20% budget: labels, selection and selected indices bit-exact; output within 1e-5."""

@@ -351,3 +351,60 @@ def test_overhead_counts_every_per_step_read():
         ref.overhead_rows(n=1000, rows=100.0, clusters=256.0, d=128, fitted=True)
     f = ref.kv_read_fraction(n=1000, rows=200.0, clusters=64.0, d=16, summary_bits=8)
     assert abs(f - (400 + ref.overhead_rows(n=1000, rows=200.0, clusters=64.0, d=16, summary_bits=8)) / 2000) < 1e-12
+
+
+def test_post_fit_division_keeps_the_cap_and_recounts():
+    """The oracle's division after a fit (src/ssa/attn/sphere_gpu.py:307-391): every cluster ends
+    at or under the cap (spare slots permitting), counts equal the label histogram, summaries
+    equal a float64 recount, and labels stay below the clusters in use."""
+    g = np.random.default_rng(3)
+    d, n, C, C_init = 32, 1500, 64, 8
+    centers = g.standard_normal((5, d))
+    which = g.choice(5, n, p=[0.5, 0.2, 0.15, 0.1, 0.05])
+    K = (centers[which] * 4 + g.standard_normal((n, d))).astype(np.float32)[None]
+    c = CanonIndex(1, d, C=C, capacity=n + 8, C_init=C_init, partition="kmeans", summary_bits=8)
+    start, end = 1, n
+    init = np.arange(C_init, dtype=np.int32) * ((end - start) // C_init)
+    c.build(K, start=start, end=end, fit=True, iters=10, init_idx=init)
+    cap = np.float32(2.0 * (end - start) / C_init)
+    c.cap[:] = cap
+    assert c.count[0].max() > cap                                  # something to divide
+    rounds = c.split_after_fit(K, start=start, end=end, split_factor=2.0)
+    assert rounds >= 2
+    n_c = int(c.n_c[0])
+    assert n_c > C_init and int(c.nsplit[0]) == n_c - C_init
+    lab = c.labels[0, start:end].astype(np.int64)
+    assert lab.max() < n_c
+    assert np.array_equal(np.bincount(lab, minlength=C), c.count[0])
+    assert np.all(c.count[0] <= cap) or n_c == C
+    Kr = K[0, start:end].astype(np.float64) - c.mu_ref[0].astype(np.float64)
+    mag = np.linalg.norm(Kr, axis=1)
+    kn = Kr / np.maximum(mag, 1e-12)[:, None]
+    for s in range(n_c):
+        m = lab == s
+        np.testing.assert_allclose(c.sum_dir[0, s], kn[m].sum(0), rtol=0, atol=1e-4)
+        assert np.isclose(c.mmax[0, s], mag[m].max(), rtol=1e-6) and np.isclose(c.mmin[0, s], mag[m].min(), rtol=1e-6)
+        np.testing.assert_allclose(np.linalg.norm(c.cent[0, s]), 1.0, atol=1e-6)
+
+
+def test_post_fit_kmeans_round_finds_obvious_parts():
+    """One cluster holding three tight, well separated groups, cap a third of it: the k-means round
+    asks for ceil(count * 2 / cap) = 6 parts, started from members 0, 20, ..., 100 (two in each
+    group), so every part lies inside one group and every group is covered."""
+    d, per = 16, 40
+    dirs = np.eye(d, dtype=np.float32)[:3] * 10
+    g = np.random.default_rng(4)
+    K = np.concatenate([dirs[i] + 0.01 * g.standard_normal((per, d)) for i in range(3)]).astype(np.float32)
+    K = np.concatenate([np.zeros((1, d), np.float32), K])[None]           # position 0 is the sink
+    n = K.shape[1]
+    c = CanonIndex(1, d, C=16, capacity=n, C_init=1, partition="kmeans", summary_bits=8)
+    c.build(K, start=1, end=n, fit=True, iters=10, init_idx=np.zeros(1, np.int32))
+    assert int(c.count[0, 0]) == 3 * per
+    c.cap[:] = np.float32(per)
+    c.split_after_fit(K, start=1, end=n, split_factor=2.0)
+    lab = c.labels[0, 1:n]
+    groups = [set(lab[i * per:(i + 1) * per].tolist()) for i in range(3)]
+    assert all(not (groups[i] & groups[j]) for i in range(3) for j in range(i + 1, 3))   # no part mixes groups
+    n_c = int(c.n_c[0])
+    assert set.union(*groups) == set(range(n_c)) and 3 <= n_c <= 6
+    assert np.all(c.count[0, :n_c] <= per)
