@@ -189,34 +189,166 @@ __global__ __launch_bounds__(kT) void kmeans_init_kernel(BuildArgs A) {
 
 // assign_j = argmax over the first n_c centroids of cdot(xn_j, cent_c), lowest index on ties.
 // With write_labels the result also becomes the key's label.
+//
+// The contraction runs on the matrix cores: each wave scores groups of 16 keys against every
+// centroid with v_mfma_f32_16x16x32_bf16 on bf16 copies of the unit vectors (fp32 accumulation),
+// the centroids staged through LDS in chunks of kAsgCH. For unit x and c, bf16 rounding (relative
+// error at most 2^-9 per element) moves the score by at most 2^-8 + 2^-18, and the two fp32
+// accumulations differ from the exact dot by under 2 d 2^-24: under 0.005 in all. So every
+// centroid whose canonical dot equals the best lies within kAssignMargin = 0.02 > 2 * 0.005 of
+// the best bf16 score. A second pass rescores those candidates with the canonical dot and takes
+// the best, lowest index on ties: the result is the canonical argmax.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr float kAssignMargin = 0.02f;
+constexpr int kAsgCH = 64;                                   // centroids per LDS chunk
+template <int D> constexpr int asg_groups() { return D <= 128 ? 4 : 2; }   // 16-key groups per wave
+template <int D> constexpr int asg_keys() { return 16 * asg_groups<D>() * kW; }
+
+// 8 consecutive fp32 values [k0, k0 + 8) of a row of D, as bf16 (zeros past D)
+template <int D>
+__device__ __forceinline__ bf16x8 frag8(const float* row, int k0) {
+  bf16x8 v;
+  if (k0 < D) {
+    const float4 x = *reinterpret_cast<const float4*>(row + k0);
+    const float4 y = *reinterpret_cast<const float4*>(row + k0 + 4);
+    v[0] = (__bf16)x.x; v[1] = (__bf16)x.y; v[2] = (__bf16)x.z; v[3] = (__bf16)x.w;
+    v[4] = (__bf16)y.x; v[5] = (__bf16)y.y; v[6] = (__bf16)y.z; v[7] = (__bf16)y.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (__bf16)0.f;
+  }
+  return v;
+}
+
+// max over the 16 lanes of a DPP row, on every lane of the row
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+  return v;
+}
+// (score, index) argmax over the 16 lanes of a DPP row (lowest index on ties), on every lane
+template <int CTRL>
+__device__ __forceinline__ void row16_argmax_step(float& s, int& i) {
+  const float s2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), CTRL, 0xF, 0xF, true));
+  const int i2 = __builtin_amdgcn_mov_dpp(i, CTRL, 0xF, 0xF, true);
+  argmax_merge(s, i, s2, i2);
+}
+__device__ __forceinline__ void row16_argmax(float& s, int& i) {
+  row16_argmax_step<0xB1>(s, i);
+  row16_argmax_step<0x4E>(s, i);
+  row16_argmax_step<0x141>(s, i);
+  row16_argmax_step<0x140>(s, i);
+}
+
 template <int D>
 __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_labels) {
-  constexpr int CT = 32;
-  __shared__ float tile[CT][D];
-  const int s = blockIdx.y, h = A.b.heads[s], tid = threadIdx.x;
-  const int j = blockIdx.x * kT + tid;
+  constexpr int KS = (D + 31) / 32;                      // MFMA k-steps
+  constexpr int KG = asg_groups<D>();
+  constexpr int DP = 32 * KS + 8;                        // LDS row in bf16: 16 bytes of pad per row
+  __shared__ __align__(16) __bf16 cl[kAsgCH * DP];
+  const int s = blockIdx.y, h = A.b.heads[s], tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nc = A.st.n_c[h];
   const float* cent = A.st.shared_dirs ? A.st.cent : A.st.cent + (int64_t)h * A.st.C * D;
-  float x[D];
-  const bool ok = j < A.nb;
-  const float* xr = A.b.xn + ((int64_t)s * A.nb + (ok ? j : 0)) * D;
+  const float* xn = A.b.xn + (int64_t)s * A.nb * D;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int j0 = blockIdx.x * asg_keys<D>() + wave * 16 * KG;
+  // A operands: key j0 + 16 g + r16, elements 32 ks + 8 g4 + [0, 8)
+  bf16x8 af[KG][KS];
 #pragma unroll
-  for (int i = 0; i < D; ++i) x[i] = xr[i];
-  float best = 0.f;
-  int bi = -1;
-  for (int c0 = 0; c0 < nc; c0 += CT) {
-    const int nt = min(CT, nc - c0);
+  for (int g = 0; g < KG; ++g) {
+    const float* xa = xn + (int64_t)min(j0 + 16 * g + r16, A.nb - 1) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) af[g][ks] = frag8<D>(xa, 32 * ks + 8 * g4);
+  }
+  auto stage = [&](int c0) {
     __syncthreads();
-    for (int e = tid; e < nt * D; e += kT) tile[e / D][e % D] = cent[(int64_t)(c0 + e / D) * D + e % D];
+    for (int e = tid; e < kAsgCH * 4 * KS; e += kT) {
+      const int r = e / (4 * KS), k0 = 8 * (e % (4 * KS)), c = c0 + r;
+      bf16x8 v;
+      if (c < nc) v = frag8<D>(cent + (int64_t)c * D, k0);
+      else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (__bf16)0.f;
+      }
+      *reinterpret_cast<bf16x8*>(cl + r * DP + k0) = v;
+    }
     __syncthreads();
-    for (int r = 0; r < nt; ++r) {
-      const float sc = cdot([&](int i) { return x[i]; }, [&](int i) { return tile[r][i]; }, D);
-      if (bi < 0 || sc > best) { best = sc; bi = c0 + r; }
+  };
+  // scores of centroids c0 + 16 t + r16 against rows 4 g4 + i of every key group
+  auto tile = [&](int t, f32x4 (&acc)[KG]) {
+#pragma unroll
+    for (int g = 0; g < KG; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(cl + (16 * t + r16) * DP + 32 * ks + 8 * g4);
+#pragma unroll
+      for (int g = 0; g < KG; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g][ks], b, acc[g], 0, 0, 0);
+    }
+  };
+  // pass 1: best bf16 score of every key
+  float mx[KG][4];
+#pragma unroll
+  for (int g = 0; g < KG; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx[g][i] = -INFINITY;
+  for (int c0 = 0; c0 < nc; c0 += kAsgCH) {
+    stage(c0);
+    const int nt = min(kAsgCH / 16, (nc - c0 + 15) / 16);
+    for (int t = 0; t < nt; ++t) {
+      f32x4 acc[KG];
+      tile(t, acc);
+      const bool ok = c0 + 16 * t + r16 < nc;
+#pragma unroll
+      for (int g = 0; g < KG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx[g][i] = fmaxf(mx[g][i], ok ? acc[g][i] : -INFINITY);
     }
   }
-  if (!ok) return;
-  A.b.assign[(int64_t)s * A.nb + j] = bi;
-  if (write_labels) A.st.labels[(int64_t)h * A.st.capacity + A.b.start + j] = (int16_t)bi;
+#pragma unroll
+  for (int g = 0; g < KG; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx[g][i] = row16_max(mx[g][i]) - kAssignMargin;
+  // pass 2: canonical rescoring of the candidates
+  float best[KG][4];
+  int bi[KG][4];
+#pragma unroll
+  for (int g = 0; g < KG; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { best[g][i] = 0.f; bi[g][i] = -1; }
+  for (int c0 = 0; c0 < nc; c0 += kAsgCH) {
+    stage(c0);
+    const int nt = min(kAsgCH / 16, (nc - c0 + 15) / 16);
+    for (int t = 0; t < nt; ++t) {
+      f32x4 acc[KG];
+      tile(t, acc);
+      const int c = c0 + 16 * t + r16;
+      const float* cr = cent + (int64_t)min(c, nc - 1) * D;
+#pragma unroll
+      for (int g = 0; g < KG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (c < nc && acc[g][i] >= mx[g][i]) {
+            const float* xr = xn + (int64_t)min(j0 + 16 * g + 4 * g4 + i, A.nb - 1) * D;
+            argmax_merge(best[g][i], bi[g][i], cdot_ptr(xr, cr, D), c);
+          }
+        }
+    }
+  }
+  // lane r16 == i of row group g4 writes key j0 + 16 g + 4 g4 + i
+#pragma unroll
+  for (int g = 0; g < KG; ++g)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      row16_argmax(best[g][i], bi[g][i]);
+      const int j = j0 + 16 * g + 4 * g4 + i;
+      if (r16 == i && j < A.nb) {
+        A.b.assign[(int64_t)s * A.nb + j] = bi[g][i];
+        if (write_labels) A.st.labels[(int64_t)h * A.st.capacity + A.b.start + j] = (int16_t)bi[g][i];
+      }
+    }
 }
 
 // Blocked sums, stage 1: for block b of kKB consecutive keys, per cluster, the ordered sum of its
@@ -657,12 +789,15 @@ extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b,
     else normalize(0.f);
     hipLaunchKernelGGL(rbar_kernel, dim3(b->n_sel), dim3(64), 0, s, A);
     auto assign = [&](int write_labels) {
+      auto go = [&](auto kern, int keys) {
+        hipLaunchKernelGGL(kern, dim3((A.nb + keys - 1) / keys, b->n_sel), dim3(kT), 0, s, A, write_labels);
+      };
       switch (st->d) {
-        case 16: hipLaunchKernelGGL(assign_kernel<16>, gk, dim3(kT), 0, s, A, write_labels); break;
-        case 32: hipLaunchKernelGGL(assign_kernel<32>, gk, dim3(kT), 0, s, A, write_labels); break;
-        case 64: hipLaunchKernelGGL(assign_kernel<64>, gk, dim3(kT), 0, s, A, write_labels); break;
-        case 128: hipLaunchKernelGGL(assign_kernel<128>, gk, dim3(kT), 0, s, A, write_labels); break;
-        case 256: hipLaunchKernelGGL(assign_kernel<256>, gk, dim3(kT), 0, s, A, write_labels); break;
+        case 16: go(assign_kernel<16>, asg_keys<16>()); break;
+        case 32: go(assign_kernel<32>, asg_keys<32>()); break;
+        case 64: go(assign_kernel<64>, asg_keys<64>()); break;
+        case 128: go(assign_kernel<128>, asg_keys<128>()); break;
+        case 256: go(assign_kernel<256>, asg_keys<256>()); break;
       }
     };
     if (b->fit && !st->shared_dirs) {

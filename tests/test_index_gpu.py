@@ -82,6 +82,46 @@ def test_prefill_random_partition_is_bit_exact():
     _same(idx, _canon_like(idx, K, 1200))
 
 
+def test_prefill_duplicate_seeds_tie_to_the_lowest_index():
+    """Fewer binned keys than seeds: the seed list cycles (src/ssa/attn/clusterkv.py:34-35), so
+    centroids c and c + nb start equal and every assignment between them is an exact tie, which
+    the matrix-core assignment must settle as the canonical argmax does (lowest index)."""
+    K, V, q = _keys(2, 16 + 1 + 40, seed=4)
+    idx = _fused()
+    idx.observe(K, 57)
+    canon = _canon_like(idx, K, 57)
+    _same(idx, canon)
+    assert int(canon.count[:, 40:].sum()) == 0
+
+
+def test_prefill_exact_ties_against_axis_directions():
+    """Keys on the diagonals of the first coordinate axes, in +/- pairs so that the binned mean is
+    exactly zero: each key's best axes score exactly the same, and the label must be the lowest
+    of them (bf16 copies of such keys score the tied axes equally too, and the rescoring breaks
+    the tie by index)."""
+    g = torch.Generator().manual_seed(5)
+    H_kv, d, n = 2, 128, 16 + 1 + 2 * 300
+    K = torch.zeros(H_kv, n, d)
+    for h in range(H_kv):
+        for p in range(300):
+            k = torch.zeros(d)
+            axes = torch.randperm(64, generator=g)[: int(torch.randint(1, 4, (1,), generator=g))]
+            k[axes] = float(torch.randint(1, 3, (1,), generator=g))
+            K[h, 1 + 2 * p], K[h, 2 + 2 * p] = k, -k
+        K[h, 0] = torch.randn(d, generator=g)
+        K[h, 1 + 600:] = torch.randn(16, d, generator=g)
+    K = K.to(torch.bfloat16).cuda()
+    idx = _fused(partition="random", kind="cross", C=64)
+    idx.observe(K, n)
+    canon = _canon_like(idx, K, n)
+    _same(idx, canon)
+    lab = canon.labels[:, 1:601]
+    keys = K[:, 1:601].float().cpu().numpy()
+    for h in range(H_kv):
+        pos = keys[h, ::2, :64]
+        assert np.array_equal(lab[h, ::2], np.argmax(pos, axis=1))          # first of the tied maxima
+
+
 @pytest.mark.parametrize("summary_bits", [8, 32])
 def test_insertion_is_bit_exact(summary_bits):
     K, V, q = _keys(4, 1600, seed=3)
