@@ -157,8 +157,8 @@ typedef struct ssa_build_args {
   float* xn; float* mag;     /* scratch [n_sel, end-start, d] and [n_sel, end-start] */
   float* sq;                 /* scratch [n_sel, end-start] */
   int32_t* assign;           /* scratch [n_sel, end-start] */
-  float* part;               /* scratch [n_sel, nblocks, C_fit, d], nblocks = ceil((end-start)/256) */
-  int32_t* part_cnt;         /* scratch [n_sel, nblocks, C_fit] */
+  float* part;               /* scratch [n_sel, nblocks, max(C, C_fit), d], nblocks = ceil((end-start)/256) */
+  int32_t* part_cnt;         /* scratch [n_sel, nblocks, max(C, C_fit)] */
   const int32_t* init_idx;   /* [C_fit] k-means seed members (offsets into the range) */
   int32_t fit;               /* 1: k-means fit of C_fit clusters first; 0: keep the centroids */
   int32_t C_fit; int32_t iters;

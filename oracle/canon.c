@@ -23,7 +23,8 @@
  *   exp(x<=0)  Cody-Waite by ln2 (hi 0.693145751953125, lo 1.42860682030941723e-6), degree-7
  *              Taylor in Horner form with fma, times 2^k; 0 below -87
  *   sums       left to right from +0; softmax denominators as a pairwise tree over the C slots;
- *              prefill sums in blocks of 256 keys (each block left to right), then over blocks
+ *              prefill sums (key sum, squared lengths, cluster sums) in blocks of 256 keys (each
+ *              block left to right from +0), then the block sums left to right from +0
  * Build: oracle/Makefile (gcc -O3 -mfma -ffp-contract=off, so only the explicit fmaf are fused).
  */
 #include <math.h>
@@ -523,9 +524,15 @@ void canon_build(canon_head_t* H, const float* K, int start, int end, const floa
                  const int32_t* init_idx) {
   const int d = H->d, C = H->C, nb = end - start;
   float* ks = H->ksum;
+  /* ksum: per block of KB consecutive keys a left-to-right sum, then the block sums left to right */
   for (int i = 0; i < d; ++i) {
     float s = 0.f;
-    for (int p = start; p < end; ++p) s = s + K[(int64_t)p * d + i];
+    for (int b0 = start; b0 < end; b0 += KB) {
+      const int b1 = b0 + KB < end ? b0 + KB : end;
+      float sb = 0.f;
+      for (int p = b0; p < b1; ++p) sb = sb + K[(int64_t)p * d + i];
+      s = s + sb;
+    }
     ks[i] = s;
     H->mu_ref[i] = mu ? mu[i] : (nb > 0 ? s / (float)nb : 0.f);
   }
@@ -538,14 +545,15 @@ void canon_build(canon_head_t* H, const float* K, int start, int end, const floa
     float* mag = (float*)malloc(sizeof(float) * nb);
     float* kr = (float*)malloc(sizeof(float) * d);
     int* as = (int*)malloc(sizeof(int) * nb);
-    float tsq = 0.f;
+    float tsq = 0.f, tb = 0.f;     /* squared lengths: block sums of KB keys, added left to right */
     for (int j = 0; j < nb; ++j) {
       for (int i = 0; i < d; ++i) kr[i] = K[(int64_t)(start + j) * d + i] - H->mu_ref[i];
       const float sq = canon_dot(kr, kr, d);
       mag[j] = sqrtf(sq);
       const float magc = fmaxf(mag[j], 1e-12f);
       for (int i = 0; i < d; ++i) xn[(int64_t)j * d + i] = kr[i] / magc;
-      tsq = tsq + sq;
+      tb = tb + sq;
+      if ((j + 1) % KB == 0 || j + 1 == nb) { tsq = tsq + tb; tb = 0.f; }
     }
     *H->rbar = sqrtf(tsq / (float)nb);
     if (fit && !H->shared_dirs) {

@@ -98,24 +98,36 @@ __device__ __forceinline__ const char* head_keys(const BuildArgs& A, int h) {
   return reinterpret_cast<const char*>(A.b.k) + (int64_t)elem_size(A.b.k_dtype) * (int64_t)h * A.b.s_kh;
 }
 
-// Centre: ksum = ordered sum of the range's keys, mu = given or ksum / nb; reset the summaries.
+// Centre, stage 1: per block b of kKB consecutive keys of the range, the left-to-right sum of its
+// keys, into part[s][b][0][:].
 template <typename T>
-__global__ __launch_bounds__(kT) void center_kernel(BuildArgs A) {
+__global__ __launch_bounds__(kT) void center_part_kernel(BuildArgs A, int ncl) {
+  const int s = blockIdx.y, h = A.b.heads[s], b = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  if (tid >= d) return;
+  KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
+  const int p0 = A.b.start + b * kKB, p1 = min(p0 + kKB, A.b.end);
+  // loads are issued 32 positions ahead of the adds
+  float ks = 0.f;
+  int p = p0;
+  for (; p + 32 <= p1; p += 32) {
+    float v[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) v[u] = K(p + u, tid);
+#pragma unroll
+    for (int u = 0; u < 32; ++u) ks = ks + v[u];
+  }
+  for (; p < p1; ++p) ks = ks + K(p, tid);
+  A.b.part[(((int64_t)s * A.nblk + b) * ncl) * d + tid] = ks;
+}
+
+// Centre, stage 2: ksum = left-to-right sum of the block sums, mu = given or ksum / nb; reset the
+// summaries.
+__global__ __launch_bounds__(kT) void center_kernel(BuildArgs A, int ncl) {
   const int s = blockIdx.x, h = A.b.heads[s], tid = threadIdx.x;
   const int d = A.st.d, C = A.st.C, nb = A.nb;
-  KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
   if (tid < d) {
-    // left-to-right sum; loads are issued 32 positions ahead of the adds
     float ks = 0.f;
-    int p = A.b.start;
-    for (; p + 32 <= A.b.end; p += 32) {
-      float v[32];
-#pragma unroll
-      for (int u = 0; u < 32; ++u) v[u] = K(p + u, tid);
-#pragma unroll
-      for (int u = 0; u < 32; ++u) ks = ks + v[u];
-    }
-    for (; p < A.b.end; ++p) ks = ks + K(p, tid);
+    for (int b = 0; b < A.nblk; ++b) ks = ks + A.b.part[(((int64_t)s * A.nblk + b) * ncl) * d + tid];
     A.st.ksum[(int64_t)h * d + tid] = ks;
     float mu;
     if (A.b.mu) mu = A.b.mu[(int64_t)s * d + tid];
@@ -139,43 +151,48 @@ __global__ __launch_bounds__(kT) void center_kernel(BuildArgs A) {
 }
 
 // Unit centred directions of the range's keys, their lengths and squared lengths.
+// Also, per block of kKB (= kT) keys, the left-to-right sum of their squared lengths, into
+// part[s][b][1][0].
 template <typename T, int D>
-__global__ __launch_bounds__(kT) void normalize_kernel(BuildArgs A) {
+__global__ __launch_bounds__(kT) void normalize_kernel(BuildArgs A, int ncl) {
+  static_assert(kKB == kT, "one block of the squared-length sums per workgroup");
+  __shared__ float s_sq[kT];
   const int s = blockIdx.y, h = A.b.heads[s];
   const int j = blockIdx.x * kT + threadIdx.x;
-  if (j >= A.nb) return;
-  KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
-  const float* mu = A.st.mu_ref + (int64_t)h * D;
-  const int p = A.b.start + j;
-  float kr[D];
+  float sq = 0.f;
+  if (j < A.nb) {
+    KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
+    const float* mu = A.st.mu_ref + (int64_t)h * D;
+    const int p = A.b.start + j;
+    float kr[D];
 #pragma unroll
-  for (int i = 0; i < D; ++i) kr[i] = K(p, i) - mu[i];
-  const float sq = cdot([&](int i) { return kr[i]; }, [&](int i) { return kr[i]; }, D);
-  const float mag = sqrtf(sq);
-  const float magc = fmaxf(mag, 1e-12f);
-  float4* x = reinterpret_cast<float4*>(A.b.xn + ((int64_t)s * A.nb + j) * D);
+    for (int i = 0; i < D; ++i) kr[i] = K(p, i) - mu[i];
+    sq = cdot([&](int i) { return kr[i]; }, [&](int i) { return kr[i]; }, D);
+    const float mag = sqrtf(sq);
+    const float magc = fmaxf(mag, 1e-12f);
+    float4* x = reinterpret_cast<float4*>(A.b.xn + ((int64_t)s * A.nb + j) * D);
 #pragma unroll
-  for (int k = 0; k < D / 4; ++k)
-    x[k] = make_float4(kr[4 * k] / magc, kr[4 * k + 1] / magc, kr[4 * k + 2] / magc, kr[4 * k + 3] / magc);
-  A.b.mag[(int64_t)s * A.nb + j] = mag;
-  A.b.sq[(int64_t)s * A.nb + j] = sq;
+    for (int k = 0; k < D / 4; ++k)
+      x[k] = make_float4(kr[4 * k] / magc, kr[4 * k + 1] / magc, kr[4 * k + 2] / magc, kr[4 * k + 3] / magc);
+    A.b.mag[(int64_t)s * A.nb + j] = mag;
+    A.b.sq[(int64_t)s * A.nb + j] = sq;
+  }
+  s_sq[threadIdx.x] = sq;
+  __syncthreads();                                  // reached by every thread once
+  if (threadIdx.x == 0) {
+    const int nk = min(kT, A.nb - blockIdx.x * kT);
+    float t = 0.f;
+    for (int u = 0; u < nk; ++u) t = t + s_sq[u];
+    A.b.part[(((int64_t)s * A.nblk + blockIdx.x) * ncl + 1) * D] = t;
+  }
 }
 
-// rbar = sqrt(ordered sum of squared lengths / nb).
-__global__ void rbar_kernel(BuildArgs A) {
+// rbar = sqrt(left-to-right sum of the block sums of squared lengths / nb).
+__global__ void rbar_kernel(BuildArgs A, int ncl) {
   const int s = blockIdx.x, h = A.b.heads[s];
   if (threadIdx.x != 0) return;
   float t = 0.f;
-  const float* sq = A.b.sq + (int64_t)s * A.nb;
-  int j = 0;
-  for (; j + 32 <= A.nb; j += 32) {
-    float v[32];
-#pragma unroll
-    for (int u = 0; u < 32; ++u) v[u] = sq[j + u];
-#pragma unroll
-    for (int u = 0; u < 32; ++u) t = t + v[u];
-  }
-  for (; j < A.nb; ++j) t = t + sq[j];
+  for (int b = 0; b < A.nblk; ++b) t = t + A.b.part[(((int64_t)s * A.nblk + b) * ncl + 1) * A.st.d];
   A.st.rbar[h] = A.nb > 0 ? sqrtf(t / (float)A.nb) : 0.f;
 }
 
@@ -190,20 +207,24 @@ __global__ __launch_bounds__(kT) void kmeans_init_kernel(BuildArgs A) {
 // assign_j = argmax over the first n_c centroids of cdot(xn_j, cent_c), lowest index on ties.
 // With write_labels the result also becomes the key's label.
 //
-// The contraction runs on the matrix cores: each wave scores groups of 16 keys against every
-// centroid with v_mfma_f32_16x16x32_bf16 on bf16 copies of the unit vectors (fp32 accumulation),
-// the centroids staged through LDS in chunks of kAsgCH. For unit x and c, bf16 rounding (relative
-// error at most 2^-9 per element) moves the score by at most 2^-8 + 2^-18, and the two fp32
-// accumulations differ from the exact dot by under 2 d 2^-24: under 0.005 in all. So every
-// centroid whose canonical dot equals the best lies within kAssignMargin = 0.02 > 2 * 0.005 of
-// the best bf16 score. A second pass rescores those candidates with the canonical dot and takes
-// the best, lowest index on ties: the result is the canonical argmax.
+// The contraction runs on the matrix cores: each wave scores 16 KG keys against every centroid
+// with v_mfma_f32_16x16x32_bf16 on bf16 copies of the unit vectors (fp32 accumulation), the
+// centroids staged through LDS in chunks of kAsgCH. Round-to-nearest bf16 copies (relative error
+// at most 2^-9 per element) move the score of unit x and c by at most 2^-8 + 2^-18, and the two
+// fp32 accumulations differ from the exact dot by under 2 d 2^-24: under 0.004 in all. So every
+// centroid whose canonical dot equals the best lies within kAssignMargin = 0.01 > 2 * 0.004 of the
+// best bf16 score. Pass 1 finds each key's best bf16 score; pass 2 lists the candidates (bf16
+// score within the margin). A key with one candidate takes it; the candidates of the others are
+// rescored with the canonical dot, 8 lanes per candidate (lane j runs chain j), and the best
+// taken, lowest index on ties: the result is the canonical argmax.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr float kAssignMargin = 0.02f;
+constexpr float kAssignMargin = 0.01f;
 constexpr int kAsgCH = 64;                                   // centroids per LDS chunk
 template <int D> constexpr int asg_groups() { return D <= 128 ? 4 : 2; }   // 16-key groups per wave
 template <int D> constexpr int asg_keys() { return 16 * asg_groups<D>() * kW; }
+// candidate list entries per wave: room for two tiles' worth (every lane a candidate of every key row)
+template <int D> constexpr int asg_list() { return 2 * 64 * 4 * asg_groups<D>(); }
 
 // 8 consecutive fp32 values [k0, k0 + 8) of a row of D, as bf16 (zeros past D)
 template <int D>
@@ -221,40 +242,40 @@ __device__ __forceinline__ bf16x8 frag8(const float* row, int k0) {
   return v;
 }
 
-// max over the 16 lanes of a DPP row, on every lane of the row
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+// max / sum / min over the 16 lanes of a DPP row, on every lane of the row
+template <typename T, typename F>
+__device__ __forceinline__ T row16_reduce(T v, F op) {
+  auto sh = [](T x, auto ctrl) {
+    int b;
+    __builtin_memcpy(&b, &x, 4);
+    b = __builtin_amdgcn_mov_dpp(b, decltype(ctrl)::value, 0xF, 0xF, true);
+    __builtin_memcpy(&x, &b, 4);
+    return x;
+  };
+  v = op(v, sh(v, std::integral_constant<int, 0xB1>{}));
+  v = op(v, sh(v, std::integral_constant<int, 0x4E>{}));
+  v = op(v, sh(v, std::integral_constant<int, 0x141>{}));
+  v = op(v, sh(v, std::integral_constant<int, 0x140>{}));
   return v;
-}
-// (score, index) argmax over the 16 lanes of a DPP row (lowest index on ties), on every lane
-template <int CTRL>
-__device__ __forceinline__ void row16_argmax_step(float& s, int& i) {
-  const float s2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), CTRL, 0xF, 0xF, true));
-  const int i2 = __builtin_amdgcn_mov_dpp(i, CTRL, 0xF, 0xF, true);
-  argmax_merge(s, i, s2, i2);
-}
-__device__ __forceinline__ void row16_argmax(float& s, int& i) {
-  row16_argmax_step<0xB1>(s, i);
-  row16_argmax_step<0x4E>(s, i);
-  row16_argmax_step<0x141>(s, i);
-  row16_argmax_step<0x140>(s, i);
 }
 
 template <int D>
 __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_labels) {
   constexpr int KS = (D + 31) / 32;                      // MFMA k-steps
   constexpr int KG = asg_groups<D>();
+  constexpr int NK = 16 * KG;                            // keys per wave
   constexpr int DP = 32 * KS + 8;                        // LDS row in bf16: 16 bytes of pad per row
   __shared__ __align__(16) __bf16 cl[kAsgCH * DP];
+  constexpr int LIST = asg_list<D>();
+  __shared__ int lst[kW][LIST];                      // candidates: key << 16 | centroid
+  __shared__ unsigned long long rk[kW][NK];              // best (score desc, index asc) per key
+  __shared__ int kcnt[kW][NK], kfirst[kW][NK];
   const int s = blockIdx.y, h = A.b.heads[s], tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nc = A.st.n_c[h];
   const float* cent = A.st.shared_dirs ? A.st.cent : A.st.cent + (int64_t)h * A.st.C * D;
   const float* xn = A.b.xn + (int64_t)s * A.nb * D;
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int j0 = blockIdx.x * asg_keys<D>() + wave * 16 * KG;
+  const int j0 = blockIdx.x * asg_keys<D>() + wave * NK;
   // A operands: key j0 + 16 g + r16, elements 32 ks + 8 g4 + [0, 8)
   bf16x8 af[KG][KS];
 #pragma unroll
@@ -263,6 +284,7 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) af[g][ks] = frag8<D>(xa, 32 * ks + 8 * g4);
   }
+  if (lane < NK) rk[wave][lane] = ~0ull;
   auto stage = [&](int c0) {
     __syncthreads();
     for (int e = tid; e < kAsgCH * 4 * KS; e += kT) {
@@ -288,12 +310,31 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
       for (int g = 0; g < KG; ++g) acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g][ks], b, acc[g], 0, 0, 0);
     }
   };
+  // canonical rescoring of list entries [0, n): 8 lanes per entry; with `all` false only the
+  // entries of keys with more than one candidate
+  auto rescore = [&](int n, bool all) {
+    const int q = lane >> 3, jc = lane & 7;
+    for (int e0 = 0; e0 < n; e0 += 8) {
+      const int ent = e0 + q < n ? lst[wave][e0 + q] : -1;
+      const int kl = ent >> 16, c = ent & 0xFFFF;
+      const bool go = ent >= 0 && (all || kcnt[wave][kl] > 1);
+      float v = 0.f;
+      if (go) {
+        const float* xr = xn + (int64_t)(j0 + kl) * D + jc;
+        const float* cr = cent + (int64_t)c * D + jc;
+#pragma unroll 8
+        for (int m = 0; m < D / 8; ++m) v = __builtin_fmaf(xr[8 * m], cr[8 * m], v);
+      }
+      v = group8_sum(v);
+      if (go && jc == 0) atomicMin(&rk[wave][kl], rank_key(v, c));
+    }
+  };
   // pass 1: best bf16 score of every key
-  float mx[KG][4];
+  float thr[KG][4];
 #pragma unroll
   for (int g = 0; g < KG; ++g)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mx[g][i] = -INFINITY;
+    for (int i = 0; i < 4; ++i) thr[g][i] = -INFINITY;
   for (int c0 = 0; c0 < nc; c0 += kAsgCH) {
     stage(c0);
     const int nt = min(kAsgCH / 16, (nc - c0 + 15) / 16);
@@ -304,51 +345,70 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx[g][i] = fmaxf(mx[g][i], ok ? acc[g][i] : -INFINITY);
+        for (int i = 0; i < 4; ++i) thr[g][i] = fmaxf(thr[g][i], ok ? acc[g][i] : -INFINITY);
     }
   }
+  auto fmax_op = [](float a, float b) { return fmaxf(a, b); };
 #pragma unroll
   for (int g = 0; g < KG; ++g)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mx[g][i] = row16_max(mx[g][i]) - kAssignMargin;
-  // pass 2: canonical rescoring of the candidates
-  float best[KG][4];
-  int bi[KG][4];
+    for (int i = 0; i < 4; ++i) thr[g][i] = row16_reduce(thr[g][i], fmax_op) - kAssignMargin;
+  // pass 2: list the candidates; per lane, the count and the first candidate of its columns
+  int cnt[KG][4], first[KG][4];
 #pragma unroll
   for (int g = 0; g < KG; ++g)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { best[g][i] = 0.f; bi[g][i] = -1; }
+    for (int i = 0; i < 4; ++i) { cnt[g][i] = 0; first[g][i] = 0x7FFFFFFF; }
+  int n = 0;
+  bool flushed = false;
+  const unsigned long long below = (1ull << lane) - 1ull;
   for (int c0 = 0; c0 < nc; c0 += kAsgCH) {
     stage(c0);
     const int nt = min(kAsgCH / 16, (nc - c0 + 15) / 16);
     for (int t = 0; t < nt; ++t) {
+      if (n > LIST - 64 * 4 * KG) {                    // room for one tile's worth
+        rescore(n, true);
+        n = 0;
+        flushed = true;
+      }
       f32x4 acc[KG];
       tile(t, acc);
       const int c = c0 + 16 * t + r16;
-      const float* cr = cent + (int64_t)min(c, nc - 1) * D;
 #pragma unroll
       for (int g = 0; g < KG; ++g)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (c < nc && acc[g][i] >= mx[g][i]) {
-            const float* xr = xn + (int64_t)min(j0 + 16 * g + 4 * g4 + i, A.nb - 1) * D;
-            argmax_merge(best[g][i], bi[g][i], cdot_ptr(xr, cr, D), c);
-          }
+          const int kl = 16 * g + 4 * g4 + i;
+          const bool cand = c < nc && j0 + kl < A.nb && acc[g][i] >= thr[g][i];
+          cnt[g][i] += cand ? 1 : 0;
+          first[g][i] = cand ? min(first[g][i], c) : first[g][i];
+          const unsigned long long m = __ballot(cand);
+          if (cand) lst[wave][n + __popcll(m & below)] = (kl << 16) | c;
+          n += __popcll(m);
         }
     }
   }
-  // lane r16 == i of row group g4 writes key j0 + 16 g + 4 g4 + i
+  auto add_op = [](int a, int b) { return a + b; };
+  auto min_op = [](int a, int b) { return min(a, b); };
 #pragma unroll
   for (int g = 0; g < KG; ++g)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      row16_argmax(best[g][i], bi[g][i]);
-      const int j = j0 + 16 * g + 4 * g4 + i;
-      if (r16 == i && j < A.nb) {
-        A.b.assign[(int64_t)s * A.nb + j] = bi[g][i];
-        if (write_labels) A.st.labels[(int64_t)h * A.st.capacity + A.b.start + j] = (int16_t)bi[g][i];
-      }
+      const int tot = row16_reduce(cnt[g][i], add_op), fst = row16_reduce(first[g][i], min_op);
+      if (r16 == i) { kcnt[wave][16 * g + 4 * g4 + i] = tot; kfirst[wave][16 * g + 4 * g4 + i] = fst; }
     }
+  __syncthreads();
+  rescore(n, flushed);
+  __syncthreads();
+  if (lane < NK) {
+    const int j = j0 + lane;
+    if (j < A.nb) {
+      const int k = kcnt[wave][lane];
+      const int c = k == 0 ? -1 : (k == 1 && !flushed) ? kfirst[wave][lane] : (int)(unsigned int)rk[wave][lane];
+      A.b.assign[(int64_t)s * A.nb + j] = c;
+      if (write_labels) A.st.labels[(int64_t)h * A.st.capacity + A.b.start + j] = (int16_t)c;
+    }
+  }
 }
 
 // Blocked sums, stage 1: for block b of kKB consecutive keys, per cluster, the ordered sum of its
@@ -406,16 +466,27 @@ __global__ __launch_bounds__(kT) void block_reduce_kernel(BuildArgs A, int ncl, 
   __shared__ float s_r;
   __shared__ int s_n;
   const int s = blockIdx.y, h = A.b.heads[s], c = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  if (tid == 0) s_n = 0;
+  __syncthreads();
   if (tid < d) {
+    // left to right over the blocks; loads are issued 16 blocks ahead of the adds
+    const float* pp = A.b.part + ((int64_t)s * A.nblk * ncl + c) * d + tid;
+    const int64_t st = (int64_t)ncl * d;
     float acc = 0.f;
-    for (int b = 0; b < A.nblk; ++b) acc = acc + A.b.part[(((int64_t)s * A.nblk + b) * ncl + c) * d + tid];
+    int b = 0;
+    for (; b + 16 <= A.nblk; b += 16) {
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = pp[(b + u) * st];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc = acc + x[u];
+    }
+    for (; b < A.nblk; ++b) acc = acc + pp[b * st];
     v[tid] = acc;
   }
-  if (tid == 0) {
-    int n = 0;
-    for (int b = 0; b < A.nblk; ++b) n += A.b.part_cnt[((int64_t)s * A.nblk + b) * ncl + c];
-    s_n = n;
-  }
+  int n = 0;                                        // integer counts: any order
+  for (int b = tid; b < A.nblk; b += kT) n += A.b.part_cnt[((int64_t)s * A.nblk + b) * ncl + c];
+  if (n) atomicAdd(&s_n, n);
   __syncthreads();
   const int64_t row = ((int64_t)h * A.st.C + c) * d;
   if (summaries) {
@@ -767,27 +838,32 @@ extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b,
   A.nb = b->end - b->start;
   A.nblk = (A.nb + kKB - 1) / kKB;
   A.cap_value = 0.f;
-  switch (b->k_dtype) {
-    case kBF16: hipLaunchKernelGGL(center_kernel<__hip_bfloat16>, dim3(b->n_sel), dim3(kT), 0, s, A); break;
-    case kF16: hipLaunchKernelGGL(center_kernel<__half>, dim3(b->n_sel), dim3(kT), 0, s, A); break;
-    default: hipLaunchKernelGGL(center_kernel<float>, dim3(b->n_sel), dim3(kT), 0, s, A); break;
+  const int ncl = st->C;                           // part[] holds at least C slots per block
+  if (A.nb > 0) {
+    const dim3 gb(A.nblk, b->n_sel);
+    switch (b->k_dtype) {
+      case kBF16: hipLaunchKernelGGL(center_part_kernel<__hip_bfloat16>, gb, dim3(kT), 0, s, A, ncl); break;
+      case kF16: hipLaunchKernelGGL(center_part_kernel<__half>, gb, dim3(kT), 0, s, A, ncl); break;
+      default: hipLaunchKernelGGL(center_part_kernel<float>, gb, dim3(kT), 0, s, A, ncl); break;
+    }
   }
+  hipLaunchKernelGGL(center_kernel, dim3(b->n_sel), dim3(kT), 0, s, A, ncl);
   if (A.nb > 0) {
     dim3 gk((A.nb + kT - 1) / kT, b->n_sel);
     auto normalize = [&](auto tag) {
       using T = decltype(tag);
       switch (st->d) {
-        case 16: hipLaunchKernelGGL((normalize_kernel<T, 16>), gk, dim3(kT), 0, s, A); break;
-        case 32: hipLaunchKernelGGL((normalize_kernel<T, 32>), gk, dim3(kT), 0, s, A); break;
-        case 64: hipLaunchKernelGGL((normalize_kernel<T, 64>), gk, dim3(kT), 0, s, A); break;
-        case 128: hipLaunchKernelGGL((normalize_kernel<T, 128>), gk, dim3(kT), 0, s, A); break;
-        case 256: hipLaunchKernelGGL((normalize_kernel<T, 256>), gk, dim3(kT), 0, s, A); break;
+        case 16: hipLaunchKernelGGL((normalize_kernel<T, 16>), gk, dim3(kT), 0, s, A, ncl); break;
+        case 32: hipLaunchKernelGGL((normalize_kernel<T, 32>), gk, dim3(kT), 0, s, A, ncl); break;
+        case 64: hipLaunchKernelGGL((normalize_kernel<T, 64>), gk, dim3(kT), 0, s, A, ncl); break;
+        case 128: hipLaunchKernelGGL((normalize_kernel<T, 128>), gk, dim3(kT), 0, s, A, ncl); break;
+        case 256: hipLaunchKernelGGL((normalize_kernel<T, 256>), gk, dim3(kT), 0, s, A, ncl); break;
       }
     };
     if (b->k_dtype == kBF16) normalize(__hip_bfloat16{});
     else if (b->k_dtype == kF16) normalize(__half{});
     else normalize(0.f);
-    hipLaunchKernelGGL(rbar_kernel, dim3(b->n_sel), dim3(64), 0, s, A);
+    hipLaunchKernelGGL(rbar_kernel, dim3(b->n_sel), dim3(64), 0, s, A, ncl);
     auto assign = [&](int write_labels) {
       auto go = [&](auto kern, int keys) {
         hipLaunchKernelGGL(kern, dim3((A.nb + keys - 1) / keys, b->n_sel), dim3(kT), 0, s, A, write_labels);
