@@ -352,20 +352,32 @@ def batched_sweep(args, dev) -> dict:
         for b in BATCHED_BUDGETS:
             for s in sets:
                 s[3].budget = b
-            gs = capture([lambda s=s: s[3].step(s[2], s[0], s[1], s[5]) for s in sets])
+            # the step with the next key binned inside the fused launch (insert-ahead), and with
+            # a separate insertion launch before it; both leave the same state
+            ahead = {}
+            for mode in (True, False):
+                for s in sets:
+                    s[3].insert_ahead = mode
+                gs = capture([lambda s=s: s[3].step(s[2], s[0], s[1], s[5]) for s in sets])
+                time_graph(gs, args.warmup, rot, advance=advance)
+                ahead[mode] = time_graph(gs, reps, rot, advance=advance)[0]
+                del gs
+            for s in sets:
+                s[3].insert_ahead = s[3].auto_insert_ahead()
+            step_us = ahead[sets[0][3].insert_ahead]
             ga = capture([lambda s=s: _fused_only(_Shim(*s)) for s in sets])
-            time_graph(gs, args.warmup, rot, advance=advance)
-            step_us = time_graph(gs, reps, rot, advance=advance)[0]
             attn_us = time_graph(ga, reps, rot)[0]
             rows = sets[-1][3].work.cnt.tolist()
             by = attn_bytes(rows, n)
             row[f"{int(b * 100)}%"] = {
                 "step_us": round(step_us, 2), "select_attention_us": round(attn_us, 2),
+                "insert_ahead": sets[0][3].insert_ahead,
+                "step_us_insert_ahead": round(ahead[True], 2), "step_us_insert_launch": round(ahead[False], 2),
                 "rows_per_head": int(sum(rows) / len(rows)),
                 "attention_GBs": round(by / attn_us / 1e3, 1), "attention_frac": round(by / attn_us / 1e3 / PEAK_GBS, 4),
                 "step_effective_GBs": round(step_bytes(rows, n) / step_us / 1e3, 1),
                 "speedup_vs_dense": round(dense_us / step_us, 2)}
-            del gs, ga
+            del ga
         out[f"{B}x{n}"] = row
         log(json.dumps({f"{B}x{n}": row}))
         del sets, gd

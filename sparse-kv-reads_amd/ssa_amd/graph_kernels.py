@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from ._lib import check, lib, stream_ptr
-from .labeled_attn import SplitWork, attn_args, default_splits
+from .labeled_attn import SplitWork, attn_args, cu_count, default_splits
 from .sphere_fused import SphereIndexFused
 
 STACKED = ("n_c", "sum_dir", "dir8", "cent", "cent8", "mmax", "mmin", "count", "ksum", "mu_ref", "rbar", "flags",
@@ -49,9 +49,9 @@ class SphereIndexGraph(SphereIndexFused):
     """``SphereIndexFused`` for graph capture: ``step`` issues only fixed-argument kernels."""
 
     def __init__(self, *, budget: float, block_n: int = 32, compact_block: int = 1024, refit_every: int = 0,
-                 num_splits: int | None = None, insert_ahead: bool = True, **kw):
+                 num_splits: int | None = None, insert_ahead: bool | None = None, **kw):
         super().__init__(**kw)
-        self.insert_ahead = insert_ahead
+        self.insert_ahead = insert_ahead          # None: decided at prepare (auto_insert_ahead)
         self.refit_every = refit_every
         self.refits = 0
         self.budget = budget
@@ -64,19 +64,29 @@ class SphereIndexGraph(SphereIndexFused):
         that leave the window at length ``n + 1`` are binned too: every step's launch leaves the
         state binned for the next length, so ``step`` must be called at ``n + 1``, ``n + 2``, ..."""
         self.observe(K, n)
+        H_kv, d, dev = self.H_kv, self.d, self.device
+        self.G = H // H_kv
+        S = self.num_splits or default_splits(dev, H_kv)
+        self.work = SplitWork(H_kv, S, self.G, d, dev)
+        if self.insert_ahead is None:
+            self.insert_ahead = self.auto_insert_ahead()
         if self.insert_ahead and max(1, n + 1 - self.window) > self.end:
             check(lib().ssa_insert(self._state(), self._insert_args(K, n_host=n + 1), stream_ptr(self.device)),
                   "ssa_insert")
             self.end = max(1, n + 1 - self.window)
-        H_kv, d, dev = self.H_kv, self.d, self.device
-        self.G = H // H_kv
         self.end_dev.fill_(self.end)
         self.wbuf = torch.zeros(H_kv, self.C + 1, dtype=torch.float32, device=dev)
         self.wbuf[:, self.C] = 1.0
         self.need_dev = torch.zeros(H_kv, dtype=torch.int32, device=dev)
-        S = self.num_splits or default_splits(dev, H_kv)
-        self.work = SplitWork(H_kv, S, self.G, d, dev)
         self.out = torch.empty(H, d, device=dev, dtype=K.dtype)
+
+    def auto_insert_ahead(self) -> bool:
+        """Bin the next step's key inside the fused launch (one extra workgroup per head) while
+        the heads are few, where the step is latency-bound and a second launch costs more than
+        the extra workgroups; with many heads the extra workgroups compete with the row loads
+        and a separate insertion launch is cheaper (measured on MI355X: batch 8 x 8k and
+        2 x 32k gain 5-9 us per step, batch 16 x 32k and 64 x 32k lose 19-240 us)."""
+        return 4 * self.H_kv <= cu_count(self.device)
 
     def _init(self, K, n):
         super()._init(K, n)
