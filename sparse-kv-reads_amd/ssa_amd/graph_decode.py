@@ -1,0 +1,160 @@
+"""Whole decode step captured in one hipGraph (mirrors src/ssa/models/graph_decode.py:29-157).
+
+``GraphDecoder`` reruns the model's single-token forward layer by layer with the model's own
+modules, weights and KV cache, but with the position held in device memory: the rotary angles
+are gathered at that position, the new key and value are written with ``index_copy_``, and
+attention reads the current length from device memory (``DenseAttentionGraph`` or
+``SphereIndexGraph``). Nothing in the step depends on a host number that changes between
+tokens, so it is captured once and replayed with a single graph launch per token.
+
+Batching: the cache ``[B, H_kv, L, d]`` is viewed as ``[B·H_kv, L, d]`` and the queries
+``[B, H, d]`` as ``[B·H, d]`` (every (sequence, KV head) is independent), without copying.
+
+Insertion: with insert-ahead (``SphereIndexGraph.insert_ahead``, chosen per layer at
+``prepare``) each layer's step launch bins its next key; otherwise one ``AllLayerInsert`` launch
+bins every layer's key at the start of the step, as the reference's ``fused_insert`` does.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .graph_kernels import STACKED, AllLayerInsert, DenseAttentionGraph, SphereIndexGraph
+from .qwen3 import apply_rope
+
+MODES = ("dense", "cluster")
+
+
+class GraphDecoder:
+    def __init__(self, model, cache, *, mode: str = "dense", budget: float = 0.2, C: int | None = None,
+                 window: int = 64, delta: float = 0.03, check_every: int = 16, partition: str = "kmeans",
+                 C_init: int | None = None, split_factor: float | None = None, refit_every: int = 0,
+                 grow_cap: bool = False, reset_at: int = 0, summary_bits: int = 8, cap_keys: float = 0.0,
+                 fused_insert: bool = True, var_factor: float = 0.0, var_min: int = 8,
+                 insert_ahead: bool | None = None, **_):
+        cfg = model.cfg
+        # with no slot count given: 1,024 slots, 256 clusters fitted at the prompt, splitting of
+        # clusters over twice the mean size at the fit (src/ssa/models/graph_decode.py:35-43)
+        if C is None:
+            C = 1024 if partition == "kmeans" else 256
+            if partition == "kmeans":
+                C_init = 256 if C_init is None else C_init
+                split_factor = 2.0 if split_factor is None else split_factor
+        split_factor = 0.0 if split_factor is None else split_factor
+        mode = "cluster" if mode in ("sphere", "voronoi") else mode       # old names
+        if mode not in MODES:
+            raise ValueError(f"unknown mode {mode!r}")
+        self.model, self.cache, self.mode = model, cache, mode
+        self.H, self.H_kv, self.d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.B = B = cache.k[0].shape[0]
+        p = next(model.parameters())
+        dev, dtype = p.device, p.dtype
+        self.tok = torch.zeros(B, 1, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.n_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+        cap = cache.max_seq_len
+        if mode == "dense":
+            self.attn = [DenseAttentionGraph(H=B * self.H, H_kv=B * self.H_kv, d=self.d, dtype=dtype, device=dev)
+                         for _ in model.layers]
+        else:
+            self.attn = [SphereIndexGraph(budget=budget, C=C, window=window, delta=delta, capacity=cap,
+                                          check_every=check_every, partition=partition, C_init=C_init,
+                                          split_factor=split_factor, refit_every=refit_every, grow_cap=grow_cap,
+                                          reset_at=reset_at, summary_bits=summary_bits, cap_keys=cap_keys,
+                                          var_factor=var_factor, var_min=var_min, insert_ahead=insert_ahead)
+                         for _ in model.layers]
+        self.graph = None
+        self.logits = None
+        self.fused_insert = fused_insert and mode == "cluster" and window >= 1
+        self.insert_all = None
+
+    def _heads(self, c: torch.Tensor) -> torch.Tensor:
+        """Cache ``[B, H_kv, L, d]`` -> ``[B·H_kv, L, d]`` (a view)."""
+        return c.view(-1, c.shape[2], c.shape[3])
+
+    def prepare(self, n: int) -> None:
+        """Build the attention state from the first ``n`` cached positions (after the prompt)."""
+        if self.mode != "cluster":
+            return
+        for i, idx in enumerate(self.attn):
+            idx.prepare(self._heads(self.cache.k[i]), n, self.B * self.H)
+        if self.fused_insert and not all(idx.insert_ahead for idx in self.attn):
+            for idx in self.attn:                       # one insertion launch for every layer
+                idx.insert_ahead = False
+            self.insert_all = AllLayerInsert(self.attn, [self._heads(k) for k in self.cache.k[:len(self.attn)]])
+
+    def _body(self) -> torch.Tensor:
+        m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
+        self.n_dev.copy_(self.pos + 1)
+        if self.insert_all is not None:
+            self.insert_all(self.n_dev)
+        h = m.embed(self.tok)                                              # [B, 1, hidden]
+        cos = m.rope_cos.index_select(0, self.pos)
+        sin = m.rope_sin.index_select(0, self.pos)
+        for i, layer in enumerate(m.layers):
+            a = layer.attn
+            x = layer.norm1(h)
+            q = a.q_norm(a.q(x).view(B, 1, H, d)).transpose(1, 2)
+            k = a.k_norm(a.k(x).view(B, 1, H_kv, d)).transpose(1, 2)
+            v = a.v(x).view(B, 1, H_kv, d).transpose(1, 2)
+            q, k = apply_rope(q, k, cos, sin)
+            kc, vc = self.cache.k[i], self.cache.v[i]
+            kc.index_copy_(2, self.pos, k)
+            vc.index_copy_(2, self.pos, v)
+            qh = q[:, :, 0, :].reshape(B * H, d)
+            if self.mode == "dense":
+                out = self.attn[i](qh, self._heads(kc), self._heads(vc), self.n_dev)
+            else:
+                out = self.attn[i].step(qh, self._heads(kc), self._heads(vc), self.n_dev,
+                                        insert=self.insert_all is None)
+            h = h + a.o(out.reshape(B, 1, H * d))
+            h = h + layer.ffn(layer.norm2(h))
+        return m.logits(h)
+
+    def _snapshot(self):
+        """Copies of every index state tensor (the capture's warm-up runs execute real steps)."""
+        if self.mode != "cluster":
+            return None
+        return [{f: getattr(idx, f).clone() for f in STACKED if isinstance(getattr(idx, f, None), torch.Tensor)}
+                for idx in self.attn]
+
+    def _restore(self, snap) -> None:
+        if snap is None:
+            return
+        for idx, st in zip(self.attn, snap):
+            for f, t in st.items():
+                getattr(idx, f).copy_(t)
+
+    def capture(self) -> None:
+        """Record one decode step. Call after ``prepare`` and before the first ``step``. The
+        warm-up runs write a placeholder key at the current position (the first real step
+        overwrites it) and their index updates are undone."""
+        self.pos.fill_(self.cache.cur_len)
+        snap = self._snapshot()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._body()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.logits = self._body()
+        self.graph = g
+        self._restore(snap)
+        torch.cuda.synchronize()
+
+    def step(self, token: torch.Tensor, pos: int) -> torch.Tensor:
+        """Decode ``token [B, 1]`` at position ``pos``; returns logits ``[B, 1, vocab]`` (a buffer
+        the next step overwrites)."""
+        self.tok.copy_(token)
+        self.pos.fill_(pos)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.logits = self._body()
+        if self.mode == "cluster":
+            for i, idx in enumerate(self.attn):
+                idx.after_replay(self._heads(self.cache.k[i]))
+        self.cache.cur_len = pos + 1
+        return self.logits

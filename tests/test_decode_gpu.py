@@ -1,0 +1,130 @@
+"""The decode seam and the captured whole-model decode step on the GPU, on a tiny random Qwen3.
+
+Mirrors the reference's tests/test_patch_fused.py (full budget equals dense, partial budget reads
+fewer rows, untracked mode records nothing), tests/test_legacy_names.py (old names give the same
+outputs) and tests/test_graph_decode.py (graph replays equal the eager step; full budget equals
+dense)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from ssa_amd.graph_decode import GraphDecoder
+from ssa_amd.patch import install, uninstall
+from ssa_amd.qwen3 import Qwen3Config, random_model
+
+pytestmark = pytest.mark.gpu
+
+CFG = Qwen3Config(vocab_size=64, hidden_size=64, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                  head_dim=16, intermediate_size=128, max_position_embeddings=512)
+P, T = 150, 20
+
+
+def _setup(dtype=torch.float32):
+    model = random_model(CFG, dtype=dtype, device="cuda", seed=0, std=0.2)
+    ids = torch.randint(0, CFG.vocab_size, (1, P + T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(0))
+    return model, ids
+
+
+def _decode(model, ids):
+    cache = model.alloc_cache(ids.shape[1] + 1, batch=ids.shape[0])
+    out = []
+    with torch.inference_mode():
+        model(ids[:, :P], cache, start_pos=0)
+        for t in range(P, P + T):
+            out.append(model(ids[:, t:t + 1], cache)[:, -1].float())
+    return torch.stack(out)
+
+
+def test_full_budget_matches_dense():
+    model, ids = _setup()
+    want = _decode(model, ids)
+    stats = install(model, "cluster_fused", budget=1.0, C=16, window=4, delta=0.03, group="sum_share")
+    got = _decode(model, ids)
+    uninstall(model)
+    torch.testing.assert_close(got, want, rtol=1e-2, atol=1e-2)
+    assert stats.kv_read_fraction > 1.0                   # every row plus the summaries
+
+
+def test_partial_budget_reads_fewer_rows_and_stays_finite():
+    model, ids = _setup()
+    stats = install(model, "cluster_fused", budget=0.2, C=16, window=4, delta=0.03, group="sum_share")
+    got = _decode(model, ids)
+    uninstall(model)
+    assert torch.isfinite(got).all()
+    assert 0.0 < stats.read_fraction < 0.8
+    assert 0.0 < stats.kv_read_fraction < 1.0
+    # the first decode step builds the index (no head step counted), every later one advances it
+    assert stats.head_steps == (T - 1) * CFG.num_hidden_layers * CFG.num_key_value_heads
+
+
+def test_untracked_mode_records_nothing():
+    model, ids = _setup()
+    stats = install(model, "cluster_fused", budget=0.2, C=16, window=4, track_reads=False)
+    _decode(model, ids)
+    uninstall(model)
+    assert stats.steps == 0 and stats.kv_read_fraction is None
+
+
+def test_engine_op_accepts_the_old_names():
+    model, ids = _setup()
+    outs = []
+    for name in ("cluster_fused", "voronoi_fused", "sphere_fused"):
+        install(model, name, budget=0.2, C=16, window=4, capacity=256)
+        outs.append(_decode(model, ids))
+        uninstall(model)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def _graph_decode(model, ids, *, mode, capture, B=2, **kw):
+    cache = model.alloc_cache(P + T + 1, batch=B)
+    with torch.inference_mode():
+        logits = model(ids[:, :P], cache, start_pos=0, last_only=True)
+        dec = GraphDecoder(model, cache, mode=mode, **kw)
+        dec.prepare(P)
+        if capture:
+            dec.capture()
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        out = []
+        for pos in range(P, P + T):
+            lg = dec.step(tok, pos)
+            out.append(lg[:, -1].float().clone())
+            tok = ids[:, pos + 1:pos + 2] if pos + 1 < P + T else tok
+    return torch.stack(out), dec
+
+
+@pytest.mark.parametrize("mode,ahead", [("dense", None), ("cluster", True), ("cluster", False)])
+def test_graph_replays_equal_the_eager_step(mode, ahead):
+    """Cluster mode with the insertion inside each layer's step launch (insert-ahead) and with one
+    all-layer insertion launch at the start of the step."""
+    model, _ = _setup(torch.bfloat16)
+    ids = torch.randint(0, CFG.vocab_size, (2, P + T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(1))
+    kw = dict(budget=0.2, C=16, window=4, insert_ahead=ahead) if mode == "cluster" else {}
+    eager, _ = _graph_decode(model, ids, mode=mode, capture=False, **kw)
+    graph, dec = _graph_decode(model, ids, mode=mode, capture=True, **kw)
+    assert torch.equal(eager, graph)
+    assert dec.cache.cur_len == P + T
+    if mode == "cluster":
+        assert (dec.insert_all is None) == ahead
+
+
+def test_graph_full_budget_matches_dense_and_the_model():
+    model, _ = _setup(torch.float32)
+    ids = torch.randint(0, CFG.vocab_size, (2, P + T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(2))
+    dense, _ = _graph_decode(model, ids, mode="dense", capture=True)
+    full, _ = _graph_decode(model, ids, mode="cluster", capture=True, budget=1.0, C=16, window=4)
+    torch.testing.assert_close(full, dense, rtol=1e-3, atol=1e-3)
+    # the engine's own eager decode of the same tokens (dense kernel through the model's forward)
+    cache = model.alloc_cache(P + T + 1, batch=2)
+    with torch.inference_mode():
+        logits = model(ids[:, :P], cache, start_pos=0, last_only=True)
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        want = []
+        for pos in range(P, P + T):
+            want.append(model(tok, cache)[:, -1].float())
+            tok = ids[:, pos + 1:pos + 2] if pos + 1 < P + T else tok
+    torch.testing.assert_close(dense, torch.stack(want), rtol=1e-3, atol=1e-3)
