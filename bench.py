@@ -190,8 +190,12 @@ def main() -> int:
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy 256 MiB device-to-device 5 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2),
-                    help="1: the headline workload; 2: the batched sweep of configs[2] (one JSON line)")
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
+                    help="1: the headline workload; 2: the batched sweep of configs[2]; 3: whole-model Qwen3-0.6B "
+                         "decode of configs[3] (one JSON line each)")
+    ap.add_argument("--tokens", type=int, default=1024, help="config 3: tokens generated per mode")
+    ap.add_argument("--prompt", type=int, default=32768, help="config 3: prompt length per sequence")
+    ap.add_argument("--batch", type=int, default=2, help="config 3: sequences")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the clustered sparse decode step of one "
@@ -217,6 +221,9 @@ def main() -> int:
                                      "heads per sequence, d=128, bf16, 256 k-means clusters, window 64",
                                      "budgets": list(BATCHED_BUDGETS)},
                           "results": res}), flush=True)
+        return 0
+    if args.config == 3:
+        print(json.dumps(model_decode(args, dev)), flush=True)
         return 0
     global BUDGETS
     if args.budgets:
@@ -383,6 +390,80 @@ def batched_sweep(args, dev) -> dict:
         del sets, gd
         torch.cuda.empty_cache()
     return out
+
+
+MODEL_BUDGETS = (0.20, 0.05)
+
+
+def model_decode(args, dev) -> dict:
+    """Qwen3-0.6B (28 layers, hidden 1024, 16 q / 8 kv heads, d=128, vocab 151936) with
+    random bf16 weights; ``batch`` prompts of ``prompt`` random token ids run through the model
+    (exact causal attention), then ``tokens`` tokens generated greedily per mode, the whole step
+    (embedding, 28 layers, LM head) replayed as one captured graph per token. Modes: dense
+    split-K attention, and the clustered index at 20% and 5% (1,024 slots, 256 fitted at the
+    prompt, size-cap splits on, per-step insertion). Each mode starts from the same prefilled
+    cache. tokens/s = batch x tokens / wall time of the generation loop."""
+    import torch
+    from ssa_amd.graph_decode import GraphDecoder
+    from ssa_amd.qwen3 import QWEN3_0_6B, random_model
+    B, P, Tn = args.batch, args.prompt, args.tokens
+    t0 = time.time()
+    model = random_model(QWEN3_0_6B, dtype=torch.bfloat16, device=dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    ids = torch.randint(0, QWEN3_0_6B.vocab_size, (B, P), device=dev, generator=g)
+    base = model.alloc_cache(P + Tn + 1, batch=B)
+    with torch.inference_mode():
+        logits = model(ids, base, start_pos=0, last_only=True)
+    first = logits[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    log(f"config 3: model + prefill of {B} x {P} tokens in {time.time() - t0:.1f} s")
+    res = {}
+    for mode, budget in (("dense", None), ("cluster", 0.20), ("cluster", 0.05)):
+        cache = model.alloc_cache(P + Tn + 1, batch=B)
+        for i in range(len(cache.k)):
+            cache.k[i].copy_(base.k[i])
+            cache.v[i].copy_(base.v[i])
+        cache.cur_len = P
+        t1 = time.time()
+        with torch.inference_mode():
+            dec = GraphDecoder(model, cache, mode=mode, budget=budget or 0.2)
+            dec.prepare(P)
+            dec.capture()
+        torch.cuda.synchronize()
+        prep = time.time() - t1
+        tok = first.clone()
+        toks = []
+        with torch.inference_mode():
+            for pos in range(P, P + 8):                                    # warm-up steps, not timed
+                tok = dec.step(tok, pos)[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            for pos in range(P + 8, P + Tn):
+                tok = dec.step(tok, pos)[:, -1].argmax(-1, keepdim=True)
+                toks.append(tok)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t2
+        steps = Tn - 8
+        key = "dense" if mode == "dense" else f"cluster_{int(budget * 100)}%"
+        row = {"tokens_per_s": round(B * steps / wall, 1), "ms_per_step": round(wall / steps * 1e3, 4),
+               "steps": steps, "prepare_s": round(prep, 2)}
+        if mode == "cluster":
+            idx = dec.attn[0]
+            row.update({"splits_layer0": int(idx.splits), "active_clusters_layer0": round(float(idx.active_clusters), 1),
+                        "insert_ahead": bool(idx.insert_ahead)})
+        res[key] = row
+        log(f"config 3 {key}: {json.dumps(row)}")
+        del dec, cache
+        torch.cuda.empty_cache()
+    for k in list(res):
+        if k != "dense":
+            res[k]["speedup_vs_dense"] = round(res[k]["tokens_per_s"] / res["dense"]["tokens_per_s"], 3)
+    return {"metric": "configs[3] Qwen3-0.6B whole-model decode tokens/s (hipGraph step)", "unit": "tokens/s",
+            "higher_is_better": True, "n_gpus": 1, "dtype": "bf16",
+            "data": "synthetic (random-init bf16 weights, random prompt token ids)",
+            "config": {"workload": f"configs[3]: Qwen3-0.6B shape, batch {B}, prompt {P}, {Tn} tokens greedy",
+                       "batch": B, "prompt": P, "tokens": Tn, "budgets": list(MODEL_BUDGETS)},
+            "results": res}
 
 
 class _Shim:

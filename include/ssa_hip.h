@@ -40,7 +40,9 @@ typedef struct ssa_attn_args {
   int32_t* counter;                          /* [Hk] zero on first use; the kernel leaves it zero */
   void* out; int64_t s_oh; int32_t out_dtype;/* [Hk*G, d] */
   int32_t* cnt_out;                          /* optional [Hk]: rows read per KV head */
-  int32_t n_heads; int32_t G; int32_t d; int32_t S; int32_t chunk_align;
+  int32_t n_heads; int32_t G; int32_t d; int32_t S;
+  int32_t chunk_align;                       /* dense: split boundaries are multiples of it; label
+                                                scans: split s reads blocks of 256 positions b = s mod S */
 } ssa_attn_args_t;
 
 /* Label-weighted split-K decode attention with the compaction fused in: positions whose label
@@ -199,6 +201,30 @@ typedef struct ssa_split_args {
  * (src/ssa/attn/sphere_gpu.py:56-102,307-391) and SphereIndexFused._split_overflow
  * (src/ssa/kernels/sphere_fused.py:411-413). */
 int ssa_split_fit(const ssa_index_state_t* st, const ssa_split_args_t* a, void* stream);
+
+/* ---- glue of the captured whole-model decode step -----------------------------------------
+ * These have no counterpart in the reference's path: its graph decoder runs the engine's own
+ * torch modules between the attention calls (src/ssa/models/graph_decode.py:96-124). Here each
+ * replaces a run of element-wise tensor ops of one Qwen3 layer, reproducing their rounding to
+ * the storage dtype between ops. dtype: 0 fp32, 1 bf16, 2 fp16. */
+
+/* h [rows, D] (updated in place), delta [rows, D] or NULL, w [D], x [rows, D]:
+ * if delta, h = h + delta; then x = (h * rsqrt(mean(h^2) + eps)) * w (RMSNorm). */
+int ssa_rmsnorm_add(void* h, const void* delta, const void* w, void* x, int32_t rows, int32_t D, float eps,
+                    int32_t dtype, void* stream);
+
+/* qkv [B, (H + 2 Hk) d] (query, key, value heads of each sequence). Query and key heads: RMSNorm
+ * over d with q_w / k_w [d], then the half-split rotary embedding at position *pos (int64, device
+ * memory) from cos / sin tables [max_pos, d/2] fp32; queries to q_out [B H, d], keys to
+ * k_cache[b, h, *pos, :]; values copied to v_cache[b, h, *pos, :]. The caches are
+ * [B, Hk, L, d] with element strides s_cb, s_ch, s_cl and unit last stride. d even, <= 256. */
+int ssa_qk_norm_rope_cache(const void* qkv, const void* q_w, const void* k_w, const float* cos_t, const float* sin_t,
+                           const int64_t* pos, void* q_out, void* k_cache, void* v_cache, int64_t s_cb, int64_t s_ch,
+                           int64_t s_cl, int32_t B, int32_t H, int32_t Hk, int32_t d, float eps, int32_t dtype,
+                           void* stream);
+
+/* gu [rows, 2 I] (gate then up) -> out [rows, I] = round(silu(gate)) * up (SwiGLU). */
+int ssa_silu_mul(const void* gu, void* out, int32_t rows, int32_t I, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

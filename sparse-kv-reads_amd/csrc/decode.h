@@ -8,7 +8,8 @@
 // (src/ssa/kernels/graph_kernels.py:28-59).
 //
 // Design (one kernel per call, no index list in HBM):
-//   grid (S, Hk): workgroup (sp, h) owns positions [sp*chunk, (sp+1)*chunk) of KV head h.
+//   grid (S, Hk): workgroup (sp, h) owns positions [sp*chunk, (sp+1)*chunk) of KV head h (dense)
+//   or its blocks of 256 positions b = sp (mod S) (label scans).
 //   Labelled mode scans its positions' 2-byte labels, looks their weights up in an LDS copy
 //   of w, and compacts the selected positions into an LDS list (ballot + popcount), so only
 //   selected K/V rows are ever fetched. Dense mode walks its rows directly.
@@ -165,10 +166,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   const bool per_head = !DENSE && a.per_head;
 
   const int n = a.n_dev ? *a.n_dev : a.n_host;
+  // Dense: workgroup sp owns the contiguous chunk [s0, s1). Label scans: it owns the blocks of
+  // kThreads positions b = sp, sp + S, sp + 2S, ..., PER blocks per page, so that selected rows
+  // that crowd into one stretch of positions (their clusters follow the position) still spread
+  // over every workgroup of the head.
   int chunk = (n + S - 1) / S;
   chunk = (chunk + a.chunk_align - 1) / a.chunk_align * a.chunk_align;
   const int s0 = min(sp * chunk, n);
   const int s1 = min(s0 + chunk, n);
+  auto block_pos = [&](int it, int u) { return (sp + S * (PER * it + u)) * kThreads; };
   const int16_t* labrow = DENSE ? nullptr : a.labels + (int64_t)h * a.s_lh;
   // AHEAD: workgroup S of each head (one past the splits) stages the next step's insertion
   const bool stager = AHEAD && sp == S;
@@ -186,8 +192,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     if constexpr (!DENSE) {
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
-        const int j = s0 + u * kThreads + tid;
-        lbl[u] = j < s1 ? (int)labrow[j] : 0;
+        const int j = block_pos(0, u) + tid;
+        lbl[u] = j < n ? (int)labrow[j] : 0;
       }
     }
 
@@ -259,28 +265,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)h * a.s_vh + li * 8;
     int rows_read = 0;
 
-    for (int p0 = s0; p0 < s1; p0 += kPage) {
+    // pages: dense, kPage consecutive positions of [s0, s1); label scans, PER interleaved blocks
+    for (int it = 0, p0 = s0; DENSE ? p0 < s1 : block_pos(it, 0) < n; ++it, p0 += kPage) {
       const int pn = min(kPage, s1 - p0);
       int R;
       if constexpr (DENSE) {
         R = pn;
       } else {
-        if (p0 != s0) {
+        if (it > 0) {
 #pragma unroll
           for (int u = 0; u < PER; ++u) {
-            const int j = p0 + u * kThreads + tid;
-            lbl[u] = j < s1 ? (int)labrow[j] : 0;
+            const int j = block_pos(it, u) + tid;
+            lbl[u] = j < n ? (int)labrow[j] : 0;
           }
         }
         __syncthreads();   // lw ready / previous page's list consumed
-        // Position p0 + u * kThreads + tid: the list in (u, wave, lane) order is ascending.
+        // Position block_pos(it, u) + tid: the list in (u, wave, lane) order is ascending.
         bool sel[PER];
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-          const int j = u * kThreads + tid;
+          const int j = block_pos(it, u) + tid;
           lbl[u] = min(max(lbl[u], 0), a.w_len - 1);     // a bad label never indexes outside lw
           bool s = false;
-          if (j < pn) {
+          if (j < n) {
             if (per_head) {
               for (int g = 0; g < G; ++g) s |= sm.lw[g][lbl[u]] != -INFINITY;
             } else {
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
           }
           if (sel[u]) {
             const int o = total + wbase + __popcll(bal[u] & below);
-            sm.u.list.pos[o] = p0 + u * kThreads + tid;
+            sm.u.list.pos[o] = block_pos(it, u) + tid;
             if (per_head) {
               for (int g = 0; g < G; ++g) sm.u.list.rlw[g][o] = sm.lw[g][lbl[u]];
             } else {

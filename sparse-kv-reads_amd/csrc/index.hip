@@ -41,7 +41,7 @@ struct IndexSmem : InsertBase {
 // ---- selection -----------------------------------------------------------------------------
 
 template <int D, int GMAX>
-__device__ void select_phase(IndexSmem& S, const IndexArgs& A, int h, int end) {
+__device__ __forceinline__ void select_phase(IndexSmem& S, const IndexArgs& A, int h, int end) {
   const ssa_index_state_t& st = A.st;
   const ssa_select_args_t& sl = A.sel;
   const int tid = threadIdx.x, G = sl.G;
@@ -573,23 +573,26 @@ __global__ __launch_bounds__(kT) void fit_count_kernel(FitArgs A) {
 
 // S.sums[p] = ordered sum (members in position order) of the unit directions of the members in
 // part p (H.side), S.cntp[p] their number, for p < k.
-__device__ void fit_sums(FitSmem& S, const Head& H, const Keys& K, int m, int k) {
+__device__ __forceinline__ void fit_sums(FitSmem& S, const Head& H, const Keys& K, int m, int k) {
   const int tid = threadIdx.x, d = H.d;
   for (int e = tid; e < k * d; e += kT) S.sums[e / d][e % d] = 0.f;
   if (tid < k) S.cntp[tid] = 0;
   __syncthreads();
-  for (int t0 = 0; t0 < m; t0 += kTile) {
-    const int nr = min(kTile, m - t0);
-    for (int e = tid; e < nr * d; e += kT) {
-      const int r = e / d, i = e % d, j = t0 + r;
-      S.u.spl.tile[r][i] = (K(H.mem[j], i) - S.mu[i]) / fmaxf(H.smag[j], 1e-12f);
-    }
+  // member tiles as in member_sums; the next tile's keys load while this one is summed
+  const bool v16 = keys_vec16(K);
+  const int rows = MemberTile::rows(d);
+  MemberTile T;
+  if (m > 0) T.fetch(H, K, v16, m, 0);
+  for (int t0 = 0; t0 < m; t0 += rows) {
+    const int nr = min(rows, m - t0);
+    T.store(H, S.mu, S.u.spl.tile, m, t0);
     if (tid < nr) S.u.spl.tside[tid] = H.side[t0 + tid];
     __syncthreads();
+    if (t0 + rows < m) T.fetch(H, K, v16, m, t0 + rows);
     if (tid < d)
       for (int r = 0; r < nr; ++r) {
         const int p = S.u.spl.tside[r];
-        S.sums[p][tid] = S.sums[p][tid] + S.u.spl.tile[r][tid];
+        S.sums[p][tid] = S.sums[p][tid] + S.u.spl.tile[r * d + tid];
       }
     if (tid == kT - 1)
       for (int r = 0; r < nr; ++r) S.cntp[S.u.spl.tside[r]] += 1;
@@ -600,7 +603,7 @@ __device__ void fit_sums(FitSmem& S, const Head& H, const Keys& K, int m, int k)
 // Cosine k-means of the m members into k parts (_kmeans_padded): centroids start at members
 // j*m/k, `iters` updates (a part with members takes the unit of its ordered sum), then a final
 // assignment; each member's part (the best canonical dot, lowest part on ties) goes to H.side.
-__device__ void fit_kmeans(FitSmem& S, const Head& H, const Keys& K, int m, int k, int iters) {
+__device__ __forceinline__ void fit_kmeans(FitSmem& S, const Head& H, const Keys& K, int m, int k, int iters) {
   const int tid = threadIdx.x, d = H.d;
   for (int e = tid; e < k * d; e += kT) {
     const int p = e / d, i = e % d;

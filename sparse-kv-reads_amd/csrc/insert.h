@@ -16,13 +16,15 @@ namespace ssa {
 
 constexpr int kT = 256;       // threads per workgroup
 constexpr int kW = kT / 64;   // waves
-constexpr int kTile = 16;     // member rows staged in LDS by the split's ordered sums
+constexpr int kTile = 16;     // member rows of kMaxD staged in LDS by the split's ordered sums
+constexpr int kTileFloats = kTile * kMaxD;   // a tile holds kTileFloats / d rows of d
+constexpr int kGatherPer = 8; // label positions per thread per pass of the member scan
 
 // LDS of the insertion and split code. A kernel that runs them passes a struct with the members
 // of InsertSmem (its own may add more to the union u, which must hold spl).
 struct SplitTile {
-  float tile[kTile][kMaxD];
-  int tside[kTile];
+  float tile[kTileFloats];
+  int tside[kTileFloats / 8];
 };
 
 struct InsertBase {
@@ -30,6 +32,7 @@ struct InsertBase {
   float va[kMaxD], vb[kMaxD], vs[kMaxD];
   float red_f[kW];
   int red_i[kW];
+  int gcnt[kGatherPer][kW];  // member scan: hits per (position slice, wave)
   float scal[4];
   int scali[4];
   float rmx, rmn;          // summaries of the cluster a key joins
@@ -140,27 +143,130 @@ __device__ __forceinline__ float cdot_rolled(FA a, FB b, int d) {
   return ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7));
 }
 
+// Eight consecutive elements [i0, i0 + 8) of key row pos as fp32 (i0 a multiple of 8). With v16
+// (16-byte aligned rows) one 16-byte load for 2-byte keys, two for fp32; else element loads.
+__device__ __forceinline__ void load8(const Keys& K, bool v16, int pos, int i0, float (&x)[8]) {
+  const int64_t off = (int64_t)pos * K.s_kn + i0;
+  if (v16 && K.dt != kF32) {
+    const uint4 r = *reinterpret_cast<const uint4*>(K.base + off * 2);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (K.dt == kBF16) {
+        x[2 * k] = __uint_as_float(w[k] << 16);
+        x[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      } else {
+        x[2 * k] = __half2float(__ushort_as_half((unsigned short)(w[k] & 0xffffu)));
+        x[2 * k + 1] = __half2float(__ushort_as_half((unsigned short)(w[k] >> 16)));
+      }
+    }
+  } else if (v16) {
+    const float4 a = *reinterpret_cast<const float4*>(K.base + off * 4);
+    const float4 b = *reinterpret_cast<const float4*>(K.base + off * 4 + 16);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = load_as_f32(K.base, K.dt, off + j);
+  }
+}
+
+__device__ __forceinline__ bool keys_vec16(const Keys& K) {
+  const int64_t es = elem_size(K.dt);
+  return (reinterpret_cast<uintptr_t>(K.base) & 15) == 0 && ((K.s_kn * es) & 15) == 0;
+}
+
+// Canonical dots over one member's key row, two 8-element chunks loaded per round. With
+// unit, kn = (K(pos, i) - mu[i]) / magc is dotted with each of the NV vectors v[0..NV);
+// otherwise out[0] = dot(kr, kr) with kr = K(pos, i) - mu[i].
+template <int NV, bool UNIT>
+__device__ __forceinline__ void member_dots(const Keys& K, bool v16, int pos, const float* mu, float magc,
+                                            const float* const (&v)[NV], int d, float (&out)[NV]) {
+  float c[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[k][j] = 0.f;
+#pragma unroll 1
+  for (int i0 = 0; i0 < d; i0 += 16) {
+    float x[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (i0 + 8 * u < d) load8(K, v16, pos, i0 + 8 * u, x[u]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (i0 + 8 * u < d) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int i = i0 + 8 * u + j;
+          const float kr = x[u][j] - mu[i];
+          if constexpr (UNIT) {
+            const float kn = kr / magc;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) c[k][j] = __builtin_fmaf(kn, v[k][i], c[k][j]);
+          } else {
+            c[0][j] = __builtin_fmaf(kr, kr, c[0][j]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) out[k] = ((c[k][0] + c[k][1]) + (c[k][2] + c[k][3])) + ((c[k][4] + c[k][5]) + (c[k][6] + c[k][7]));
+}
+
+// Member tiles for the ordered sums: kMemberChunks 8-element chunks per thread, so a tile holds
+// kT * 8 * kMemberChunks / d member rows of d. fetch loads a tile's raw keys into registers (the
+// next tile's load overlaps the current tile's sums); store writes their unit directions
+// kn = (k - mu) / max(|k - mu|, 1e-12) into LDS, row r at tile[r * d].
+constexpr int kMemberChunks = 1;
+static_assert(kT * 8 * kMemberChunks <= kTileFloats, "member tile too large for the LDS tile");
+
+struct MemberTile {
+  float x[kMemberChunks][8];
+  __device__ __forceinline__ static int rows(int d) { return kT * 8 * kMemberChunks / d; }
+  __device__ __forceinline__ void fetch(const Head& H, const Keys& K, bool v16, int m, int t0) {
+    const int d = H.d, cpr = d / 8, nq = min(rows(d), m - t0) * cpr;
+#pragma unroll
+    for (int ch = 0; ch < kMemberChunks; ++ch) {
+      const int q = threadIdx.x + ch * kT;
+      if (q < nq) load8(K, v16, H.mem[t0 + q / cpr], 8 * (q % cpr), x[ch]);
+    }
+  }
+  __device__ __forceinline__ void store(const Head& H, const float* mu, float* tile, int m, int t0) const {
+    const int d = H.d, cpr = d / 8, nq = min(rows(d), m - t0) * cpr;
+#pragma unroll
+    for (int ch = 0; ch < kMemberChunks; ++ch) {
+      const int q = threadIdx.x + ch * kT;
+      if (q < nq) {
+        const int r = q / cpr, i0 = 8 * (q % cpr);
+        const float magc = fmaxf(H.smag[t0 + r], 1e-12f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tile[r * d + i0 + e] = (x[ch][e] - mu[i0 + e]) / magc;
+      }
+    }
+  }
+};
+
 // Ordered sums over the members of the cluster being split: for each dimension i (thread i),
 // s1 = sum of kn_j[i] over members on side 1 and s0 over side 0, left to right in member order.
 template <class SM>
-__device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K, int m, float* s0_out, float* s1_out,
-                            int& n1_out) {
-  const int tid = threadIdx.x, d = H.d;
+__device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K, bool v16, int m, float* s0_out,
+                                            float* s1_out, int& n1_out) {
+  const int tid = threadIdx.x, d = H.d, rows = MemberTile::rows(d);
   float s0 = 0.f, s1 = 0.f;
   int n1 = 0;
-  for (int t0 = 0; t0 < m; t0 += kTile) {
-    const int nr = min(kTile, m - t0);
-    for (int e = tid; e < nr * d; e += kT) {
-      const int r = e / d, i = e % d, j = t0 + r;
-      const float magc = fmaxf(H.smag[j], 1e-12f);
-      S.u.spl.tile[r][i] = (K(H.mem[j], i) - S.mu[i]) / magc;
-    }
+  MemberTile T;
+  if (m > 0) T.fetch(H, K, v16, m, 0);
+  for (int t0 = 0; t0 < m; t0 += rows) {
+    const int nr = min(rows, m - t0);
+    T.store(H, S.mu, S.u.spl.tile, m, t0);
     if (tid < nr) S.u.spl.tside[tid] = H.side[t0 + tid];
     __syncthreads();
+    if (t0 + rows < m) T.fetch(H, K, v16, m, t0 + rows);
     if (tid < d) {
       for (int r = 0; r < nr; ++r) {
-        const float x = S.u.spl.tile[r][tid];
-        if (S.u.spl.tside[r]) { s1 = s1 + x; ++n1; } else { s0 = s0 + x; }
+        const float xv = S.u.spl.tile[r * d + tid];
+        if (S.u.spl.tside[r]) { s1 = s1 + xv; ++n1; } else { s0 = s0 + xv; }
       }
     }
     __syncthreads();
@@ -174,39 +280,75 @@ __device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K,
 
 // side_j = kn_j.b > kn_j.a for every member (canonical dots), stored in H.side; returns #side 1.
 template <class SM>
-__device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K, int m, bool with_proj) {
+__device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K, bool v16, int m, bool with_proj) {
   const int tid = threadIdx.x, d = H.d;
   int n1 = 0;
   for (int j = tid; j < m; j += kT) {
     const int pos = H.mem[j];
     const float magc = fmaxf(H.smag[j], 1e-12f);
-    auto kn = [&](int i) { return (K(pos, i) - S.mu[i]) / magc; };
-    const float da = cdot_rolled(kn, [&](int i) { return S.va[i]; }, d);
-    const float db = cdot_rolled(kn, [&](int i) { return S.vb[i]; }, d);
-    const int one = db > da ? 1 : 0;
+    int one;
+    if (with_proj) {
+      const float* const v[3] = {S.va, S.vb, S.vs};
+      float o[3];
+      member_dots<3, true>(K, v16, pos, S.mu, magc, v, d, o);
+      one = o[1] > o[0] ? 1 : 0;
+      H.proj[j] = o[2];
+    } else {
+      const float* const v[2] = {S.va, S.vb};
+      float o[2];
+      member_dots<2, true>(K, v16, pos, S.mu, magc, v, d, o);
+      one = o[1] > o[0] ? 1 : 0;
+    }
     H.side[j] = one;
     n1 += one;
-    if (with_proj) H.proj[j] = cdot_rolled(kn, [&](int i) { return S.vs[i]; }, d);
   }
   return block_sum_i(S, n1);
 }
 
 // Positions of cluster c among [lo, hi), ascending, into H.mem[0 .. m) (at most H.ms); returns m.
+// Each pass scans kGatherPer * kT positions (position j0 + u * kT + tid for slice u), the next
+// pass's labels loading while this one is counted.
 template <class SM>
 __device__ __forceinline__ int gather_members(SM& S, const Head& H, int c, int lo, int hi) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  constexpr int PT = kGatherPer;
+  int lab[PT];
+  auto load = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      const int j = j0 + u * kT + tid;
+      lab[u] = j < hi ? (int)H.labels[j] : -1;
+    }
+  };
   int m = 0;
-  for (int j0 = lo; j0 < hi; j0 += kT) {
-    const int j = j0 + tid;
-    const bool hit = j < hi && H.labels[j] == c;
-    const int incl = wave_prefix_count(hit, lane);
-    if (lane == 63) S.red_i[wave] = incl;
+  if (lo < hi) load(lo);
+  for (int j0 = lo; j0 < hi; j0 += PT * kT) {
+    bool hit[PT];
+    unsigned long long bal[PT];
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      hit[u] = lab[u] == c;
+      bal[u] = __ballot(hit[u]);
+      if (lane == 0) S.gcnt[u][wave] = __popcll(bal[u]);
+    }
+    if (j0 + PT * kT < hi) load(j0 + PT * kT);
     __syncthreads();
-    int wb = 0, tot = 0;
-    for (int w2 = 0; w2 < kW; ++w2) { if (w2 < wave) wb += S.red_i[w2]; tot += S.red_i[w2]; }
-    const int slot = m + wb + incl - 1;
-    if (hit && slot < H.ms) H.mem[slot] = j;
-    m += tot;
+#pragma unroll
+    for (int u = 0; u < PT; ++u) {
+      int wb = 0, tot = 0;
+#pragma unroll
+      for (int w2 = 0; w2 < kW; ++w2) {
+        const int c2 = S.gcnt[u][w2];
+        if (w2 < wave) wb += c2;
+        tot += c2;
+      }
+      if (hit[u]) {
+        const int slot = m + wb + __popcll(bal[u] & below);
+        if (slot < H.ms) H.mem[slot] = j0 + u * kT + tid;
+      }
+      m += tot;
+    }
     __syncthreads();
   }
   return min(m, H.ms);
@@ -218,14 +360,16 @@ template <class SM>
 __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st, const Head& H, const Keys& K, int h,
                               int c, int nw, int stop) {
   const int tid = threadIdx.x, d = H.d;
+  const bool v16 = keys_vec16(K);
   // 1. members in ascending position order
   const int m = gather_members(S, H, c, 1, stop);
   if (m < 2) return;   // labels and counts disagree: leave the cluster as it is
   // 2. lengths
   for (int j = tid; j < m; j += kT) {
-    const int pos = H.mem[j];
-    auto kr = [&](int i) { return K(pos, i) - S.mu[i]; };
-    H.smag[j] = sqrtf(cdot_rolled(kr, kr, d));
+    const float* const none[1] = {nullptr};
+    float sq[1];
+    member_dots<1, false>(K, v16, H.mem[j], S.mu, 1.f, none, d, sq);
+    H.smag[j] = sqrtf(sq[0]);
   }
   __syncthreads();
   // 3. start from the first member and the member least similar to it
@@ -234,10 +378,10 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
   float lo = 0.f;
   int far = -1;
   for (int j = tid; j < m; j += kT) {
-    const int pos = H.mem[j];
-    const float magc = fmaxf(H.smag[j], 1e-12f);
-    auto kn = [&](int i) { return (K(pos, i) - S.mu[i]) / magc; };
-    argmin_merge(lo, far, cdot_rolled(kn, [&](int i) { return S.va[i]; }, d), j);
+    const float* const v[1] = {S.va};
+    float o[1];
+    member_dots<1, true>(K, v16, H.mem[j], S.mu, fmaxf(H.smag[j], 1e-12f), v, d, o);
+    argmin_merge(lo, far, o[0], j);
   }
   block_argmin(S, lo, far);
   if (tid < d) S.vb[tid] = (K(H.mem[far], tid) - S.mu[tid]) / fmaxf(H.smag[far], 1e-12f);
@@ -245,16 +389,16 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
   // 4. 2-means on cosine similarity, 4 iterations
   int n1 = 0;
   for (int it = 0; it < 4; ++it) {
-    member_sides(S, H, K, m, false);
+    member_sides(S, H, K, v16, m, false);
     __syncthreads();
-    member_sums(S, H, K, m, S.kr, S.sd, n1);
+    member_sums(S, H, K, v16, m, S.kr, S.sd, n1);
     if (m - n1 > 0) block_unit(S, S.kr, S.va, d);
     if (n1 > 0) block_unit(S, S.sd, S.vb, d);
   }
   // 5. final sides and projections on b - a
   if (tid < d) S.vs[tid] = S.vb[tid] - S.va[tid];
   __syncthreads();
-  n1 = member_sides(S, H, K, m, true);
+  n1 = member_sides(S, H, K, v16, m, true);
   const float mf = (float)m, n1f = (float)n1;
   if (n1f < 0.25f * mf || n1f > 0.75f * mf) {
     // lopsided: cut at the median projection (rank ties by member order)
@@ -271,7 +415,7 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
     __syncthreads();
   }
   // 6. both halves' summaries; relabel side 1
-  member_sums(S, H, K, m, S.kr, S.sd, n1);
+  member_sums(S, H, K, v16, m, S.kr, S.sd, n1);
   float x0 = 0.f, x1 = 0.f, y0 = INFINITY, y1 = INFINITY;
   for (int j = tid; j < m; j += kT) {
     const float mg = H.smag[j];

@@ -402,7 +402,7 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
   }
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    if (256 * k >= C) {                         // no slot of this round exists (uniform)
+    if (256 * k >= min(C, n_act)) {             // no slot of this round is in use (uniform)
       cnt[k] = 0;
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) z[k][g] = -INFINITY;

@@ -25,7 +25,7 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-fhip-fp32-correctly-rounded-divide-sqrt", f"-I{INCLUDE}"]
 SOURCES = {name: ["-ffp-contract=off"] for name in
-           ("decode_bf16.hip", "decode_f16.hip", "decode_f32.hip", "attention.hip", "index.hip")}
+           ("decode_bf16.hip", "decode_f16.hip", "decode_f32.hip", "attention.hip", "index.hip", "model.hip")}
 
 
 def _hipcc() -> str:

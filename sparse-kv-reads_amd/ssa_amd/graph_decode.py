@@ -13,12 +13,20 @@ Batching: the cache ``[B, H_kv, L, d]`` is viewed as ``[B·H_kv, L, d]`` and the
 Insertion: with insert-ahead (``SphereIndexGraph.insert_ahead``, chosen per layer at
 ``prepare``) each layer's step launch bins its next key; otherwise one ``AllLayerInsert`` launch
 bins every layer's key at the start of the step, as the reference's ``fused_insert`` does.
+
+Glue: with ``glue="fused"`` (the default) each layer is four GEMMs (q/k/v, o, gate/up, down;
+the q/k/v and gate/up weights concatenated once), the attention step, and three HIP kernels
+(``ssa_rmsnorm_add``: residual add + RMSNorm; ``ssa_qk_norm_rope_cache``: q/k RMSNorm, rotary
+embedding, KV-cache write; ``ssa_silu_mul``), instead of the ~60 element-wise launches of the
+model's own modules (``glue="torch"``, as the reference's ``_body`` runs them).
 """
 
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
+from ._lib import check, dtype_tag, lib, stream_ptr
 from .graph_kernels import STACKED, AllLayerInsert, DenseAttentionGraph, SphereIndexGraph
 from .qwen3 import apply_rope
 
@@ -31,7 +39,7 @@ class GraphDecoder:
                  C_init: int | None = None, split_factor: float | None = None, refit_every: int = 0,
                  grow_cap: bool = False, reset_at: int = 0, summary_bits: int = 8, cap_keys: float = 0.0,
                  fused_insert: bool = True, var_factor: float = 0.0, var_min: int = 8,
-                 insert_ahead: bool | None = None, **_):
+                 insert_ahead: bool | None = None, glue: str = "fused", **_):
         cfg = model.cfg
         # with no slot count given: 1,024 slots, 256 clusters fitted at the prompt, splitting of
         # clusters over twice the mean size at the fit (src/ssa/models/graph_decode.py:35-43)
@@ -49,6 +57,8 @@ class GraphDecoder:
         self.B = B = cache.k[0].shape[0]
         p = next(model.parameters())
         dev, dtype = p.device, p.dtype
+        if cache.max_seq_len > model.rope_cos.shape[0]:
+            raise ValueError("the cache is longer than the model's rotary tables")
         self.tok = torch.zeros(B, 1, dtype=torch.long, device=dev)
         self.pos = torch.zeros(1, dtype=torch.long, device=dev)
         self.n_dev = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -67,6 +77,18 @@ class GraphDecoder:
         self.logits = None
         self.fused_insert = fused_insert and mode == "cluster" and window >= 1
         self.insert_all = None
+        if glue not in ("fused", "torch"):
+            raise ValueError(f"unknown glue {glue!r}")
+        self.glue = glue
+        if glue == "fused":
+            with torch.no_grad():
+                self._wqkv = [torch.cat((l.attn.q.weight, l.attn.k.weight, l.attn.v.weight)) for l in model.layers]
+                self._wgu = [torch.cat((l.ffn.gate.weight, l.ffn.up.weight)) for l in model.layers]
+            self._x = torch.empty(B, cfg.hidden_size, device=dev, dtype=dtype)
+            self._qh = torch.empty(B * self.H, self.d, device=dev, dtype=dtype)
+            self._act = torch.empty(B, cfg.intermediate_size, device=dev, dtype=dtype)
+            self._dt = dtype_tag(dtype)
+            self._eps = float(cfg.rms_norm_eps)
 
     def _heads(self, c: torch.Tensor) -> torch.Tensor:
         """Cache ``[B, H_kv, L, d]`` -> ``[B·H_kv, L, d]`` (a view)."""
@@ -83,7 +105,46 @@ class GraphDecoder:
                 idx.insert_ahead = False
             self.insert_all = AllLayerInsert(self.attn, [self._heads(k) for k in self.cache.k[:len(self.attn)]])
 
+    def _attend(self, i, qh, kc, vc):
+        if self.mode == "dense":
+            return self.attn[i](qh, self._heads(kc), self._heads(vc), self.n_dev)
+        return self.attn[i].step(qh, self._heads(kc), self._heads(vc), self.n_dev, insert=self.insert_all is None)
+
+    def _body_fused(self) -> torch.Tensor:
+        m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
+        L, s, x, eps, dt = len(m.layers), stream_ptr(self.tok.device), self._x, self._eps, self._dt
+        self.n_dev.copy_(self.pos + 1)
+        if self.insert_all is not None:
+            self.insert_all(self.n_dev)
+        h = m.embed(self.tok).view(B, -1)                                  # the residual stream, updated in place
+        check(lib().ssa_rmsnorm_add(h.data_ptr(), None, m.layers[0].norm1.weight.data_ptr(), x.data_ptr(), B,
+                                    h.shape[1], eps, dt, s), "ssa_rmsnorm_add")
+        for i, layer in enumerate(m.layers):
+            a, f = layer.attn, layer.ffn
+            qkv = F.linear(x, self._wqkv[i])
+            kc, vc = self.cache.k[i], self.cache.v[i]
+            check(lib().ssa_qk_norm_rope_cache(qkv.data_ptr(), a.q_norm.weight.data_ptr(), a.k_norm.weight.data_ptr(),
+                                               m.rope_cos.data_ptr(), m.rope_sin.data_ptr(), self.pos.data_ptr(),
+                                               self._qh.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0),
+                                               kc.stride(1), kc.stride(2), B, H, H_kv, d, eps, dt, s),
+                  "ssa_qk_norm_rope_cache")
+            out = self._attend(i, self._qh, kc, vc)
+            o = F.linear(out.view(B, H * d), a.o.weight)
+            check(lib().ssa_rmsnorm_add(h.data_ptr(), o.data_ptr(), layer.norm2.weight.data_ptr(), x.data_ptr(), B,
+                                        h.shape[1], eps, dt, s), "ssa_rmsnorm_add")
+            gu = F.linear(x, self._wgu[i])
+            check(lib().ssa_silu_mul(gu.data_ptr(), self._act.data_ptr(), B, self._act.shape[1], dt, s),
+                  "ssa_silu_mul")
+            dn = F.linear(self._act, f.down.weight)
+            nw = m.layers[i + 1].norm1.weight if i + 1 < L else m.final_norm.weight
+            check(lib().ssa_rmsnorm_add(h.data_ptr(), dn.data_ptr(), nw.data_ptr(), x.data_ptr(), B, h.shape[1], eps,
+                                        dt, s), "ssa_rmsnorm_add")
+        head = m.embed.weight if m.lm_head is None else m.lm_head.weight
+        return F.linear(x, head).view(B, 1, -1)
+
     def _body(self) -> torch.Tensor:
+        if self.glue == "fused":
+            return self._body_fused()
         m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
         self.n_dev.copy_(self.pos + 1)
         if self.insert_all is not None:
@@ -102,11 +163,7 @@ class GraphDecoder:
             kc.index_copy_(2, self.pos, k)
             vc.index_copy_(2, self.pos, v)
             qh = q[:, :, 0, :].reshape(B * H, d)
-            if self.mode == "dense":
-                out = self.attn[i](qh, self._heads(kc), self._heads(vc), self.n_dev)
-            else:
-                out = self.attn[i].step(qh, self._heads(kc), self._heads(vc), self.n_dev,
-                                        insert=self.insert_all is None)
+            out = self._attend(i, qh, kc, vc)
             h = h + a.o(out.reshape(B, 1, H * d))
             h = h + layer.ffn(layer.norm2(h))
         return m.logits(h)
@@ -147,6 +204,8 @@ class GraphDecoder:
     def step(self, token: torch.Tensor, pos: int) -> torch.Tensor:
         """Decode ``token [B, 1]`` at position ``pos``; returns logits ``[B, 1, vocab]`` (a buffer
         the next step overwrites)."""
+        if not 0 <= pos < self.cache.max_seq_len:
+            raise ValueError("the cache is full")
         self.tok.copy_(token)
         self.pos.fill_(pos)
         if self.graph is not None:

@@ -323,7 +323,7 @@ class SphereIndexFused:
 
     def _check_flags(self, K) -> None:
         if not self.async_check:
-            self._act_on(K, self.flags.clone())                  # host sync
+            self._act_on(K, self.flags.cpu())                    # host sync
             self.flags.zero_()
             return
         if self._pending is not None:
@@ -332,7 +332,7 @@ class SphereIndexFused:
                 self._pending.synchronize()
         if self._pending is not None and self._pending.query():
             self._pending = None
-            self._act_on(K, self._flags_host.to(self.device))
+            self._act_on(K, self._flags_host.clone())          # host copy: no device sync unless a flag is set
         if self._pending is None:
             self._flags_host.copy_(self.flags, non_blocking=True)
             self._pending = torch.cuda.Event()

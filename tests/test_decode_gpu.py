@@ -128,3 +128,15 @@ def test_graph_full_budget_matches_dense_and_the_model():
             want.append(model(tok, cache)[:, -1].float())
             tok = ids[:, pos + 1:pos + 2] if pos + 1 < P + T else tok
     torch.testing.assert_close(dense, torch.stack(want), rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 3e-2)])
+def test_fused_glue_matches_the_model_modules(dtype, tol):
+    """The three glue kernels against the model's own modules run op by op (``glue="torch"``):
+    only the order of the RMSNorm mean's sum differs."""
+    model, _ = _setup(dtype)
+    ids = torch.randint(0, CFG.vocab_size, (2, P + T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(3))
+    fused, _ = _graph_decode(model, ids, mode="dense", capture=True, glue="fused")
+    ops, _ = _graph_decode(model, ids, mode="dense", capture=True, glue="torch")
+    torch.testing.assert_close(fused, ops, rtol=tol, atol=tol)
