@@ -226,6 +226,12 @@ int ssa_qk_norm_rope_cache(const void* qkv, const void* q_w, const void* k_w, co
 /* gu [rows, 2 I] (gate then up) -> out [rows, I] = round(silu(gate)) * up (SwiGLU). */
 int ssa_silu_mul(const void* gu, void* out, int32_t rows, int32_t I, int32_t dtype, void* stream);
 
+/* y [M, N] = x [M, K] W [N, K]^T for 1 <= M <= 8 (the decode batch), bf16 or fp16, fp32
+ * accumulation rounded once: a weight-streaming kernel for the projections of a decode step,
+ * where the library GEMM's tiles are mostly idle. K a multiple of 8; x and W 16-byte aligned. */
+int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

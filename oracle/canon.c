@@ -112,17 +112,26 @@ static void kn_of(const float* K, int d, const float* mu, int pos, float magc, f
   for (int i = 0; i < d; ++i) out[i] = (K[(int64_t)pos * d + i] - mu[i]) / magc;
 }
 
+/* Side sums of the members' unit directions: members in blocks of SUM_BLOCK (in member order),
+ * each block's side sums left to right from +0, then the block sums added left to right from +0. */
+#define SUM_BLOCK 16
 static void ordered_sums(const float* K, int d, const float* mu, const int* mem, const float* mag, const int* side,
                          int m, float* s0, float* s1, int* n1) {
   float* kn = (float*)malloc(sizeof(float) * d);
+  float* b0 = (float*)malloc(sizeof(float) * d);
+  float* b1 = (float*)malloc(sizeof(float) * d);
   for (int i = 0; i < d; ++i) { s0[i] = 0.f; s1[i] = 0.f; }
   *n1 = 0;
-  for (int j = 0; j < m; ++j) {
-    kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
-    if (side[j]) { for (int i = 0; i < d; ++i) s1[i] = s1[i] + kn[i]; ++*n1; }
-    else for (int i = 0; i < d; ++i) s0[i] = s0[i] + kn[i];
+  for (int jb = 0; jb < m; jb += SUM_BLOCK) {
+    for (int i = 0; i < d; ++i) { b0[i] = 0.f; b1[i] = 0.f; }
+    for (int j = jb; j < m && j < jb + SUM_BLOCK; ++j) {
+      kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
+      if (side[j]) { for (int i = 0; i < d; ++i) b1[i] = b1[i] + kn[i]; ++*n1; }
+      else for (int i = 0; i < d; ++i) b0[i] = b0[i] + kn[i];
+    }
+    for (int i = 0; i < d; ++i) { s0[i] = s0[i] + b0[i]; s1[i] = s1[i] + b1[i]; }
   }
-  free(kn);
+  free(kn); free(b0); free(b1);
 }
 
 static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {

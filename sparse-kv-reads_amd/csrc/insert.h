@@ -247,35 +247,60 @@ struct MemberTile {
   }
 };
 
-// Ordered sums over the members of the cluster being split: for each dimension i (thread i),
-// s1 = sum of kn_j[i] over members on side 1 and s0 over side 0, left to right in member order.
+// Side sums of the members' unit directions kn_j = (k_j - mu) / max(|k_j - mu|, 1e-12) for the
+// cluster being split: members in blocks of kSumBlock (member order), each block's side sums left
+// to right from +0, the block sums added left to right from +0 (s0: side 0, s1: side 1). A round
+// takes as many blocks as their partials fit in the LDS tile; within it each thread owns one
+// (block, 8-element chunk) and reads the chunk of every member of its block with 16-byte loads,
+// then thread i adds the round's block partials of dimension i in block order.
+constexpr int kSumBlock = 16;
 template <class SM>
 __device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K, bool v16, int m, float* s0_out,
                                             float* s1_out, int& n1_out) {
-  const int tid = threadIdx.x, d = H.d, rows = MemberTile::rows(d);
+  const int tid = threadIdx.x, d = H.d, cpr = d / 8;
+  const int nbr = kTileFloats / (2 * d);
+  float* part = S.u.spl.tile;                        // [2][nbr][d]
   float s0 = 0.f, s1 = 0.f;
-  int n1 = 0;
-  MemberTile T;
-  if (m > 0) T.fetch(H, K, v16, m, 0);
-  for (int t0 = 0; t0 < m; t0 += rows) {
-    const int nr = min(rows, m - t0);
-    T.store(H, S.mu, S.u.spl.tile, m, t0);
-    if (tid < nr) S.u.spl.tside[tid] = H.side[t0 + tid];
-    __syncthreads();
-    if (t0 + rows < m) T.fetch(H, K, v16, m, t0 + rows);
-    if (tid < d) {
-      for (int r = 0; r < nr; ++r) {
-        const float xv = S.u.spl.tile[r * d + tid];
-        if (S.u.spl.tside[r]) { s1 = s1 + xv; ++n1; } else { s0 = s0 + xv; }
+  for (int j0 = 0; j0 < m; j0 += nbr * kSumBlock) {
+    const int nb = min(nbr, (m - j0 + kSumBlock - 1) / kSumBlock);
+    for (int it = tid; it < nb * cpr; it += kT) {
+      const int b = it / cpr, i0 = 8 * (it % cpr);
+      const int jb = j0 + b * kSumBlock, je = min(jb + kSumBlock, m);
+      float a0[8], a1[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { a0[e] = 0.f; a1[e] = 0.f; }
+#pragma unroll 2
+      for (int j = jb; j < je; ++j) {
+        float x[8];
+        load8(K, v16, H.mem[j], i0, x);
+        const float magc = fmaxf(H.smag[j], 1e-12f);
+        const bool one = H.side[j] != 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float kn = (x[e] - S.mu[i0 + e]) / magc;
+          if (one) a1[e] = a1[e] + kn; else a0[e] = a0[e] + kn;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        part[b * d + i0 + e] = a0[e];
+        part[(nbr + b) * d + i0 + e] = a1[e];
       }
     }
     __syncthreads();
+    if (tid < d)
+      for (int b = 0; b < nb; ++b) {
+        s0 = s0 + part[b * d + tid];
+        s1 = s1 + part[(nbr + b) * d + tid];
+      }
+    __syncthreads();
   }
+  int n1 = 0;
+  for (int j = tid; j < m; j += kT) n1 += H.side[j] != 0 ? 1 : 0;
+  n1 = block_sum_i(S, n1);
   if (tid < d) { s0_out[tid] = s0; s1_out[tid] = s1; }
-  if (tid == 0) S.scali[1] = n1;
   __syncthreads();
-  n1_out = S.scali[1];
-  __syncthreads();
+  n1_out = n1;
 }
 
 // side_j = kn_j.b > kn_j.a for every member (canonical dots), stored in H.side; returns #side 1.

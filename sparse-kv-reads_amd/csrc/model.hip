@@ -113,6 +113,66 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu,
   }
 }
 
+// y [M, N] = x [M, K] . W[N, K]^T for a handful of rows M (decode batch): a weight-streaming
+// kernel. Wave w of workgroup b owns output columns n0 = (4 b + w) R .. n0 + R; every lane
+// reads 16 bytes (8 elements) of each of the R weight rows per k-step of 512 elements and dots
+// them with the matching 8 elements of the M rows of x (fp32 accumulation), then the 64 lane
+// partials are summed by a shuffle tree and rounded once to the output dtype.
+template <typename T, int MM, int R>
+__global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, const T* __restrict__ W,
+                                                     T* __restrict__ y, int M, int N, int K) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * R;
+  if (n0 >= N) return;
+  float acc[R][MM];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = 0.f;
+  auto widen = [](const uint4& q, float (&f)[8]) {
+    const T* h = reinterpret_cast<const T*>(&q);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = to_f32(h[e]);
+  };
+#pragma unroll 2
+  for (int k0 = 8 * lane; k0 < K; k0 += 512) {
+    uint4 wq[R], xq[MM];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      wq[r] = n0 + r < N ? *reinterpret_cast<const uint4*>(W + (int64_t)(n0 + r) * K + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      xq[m] = m < M ? *reinterpret_cast<const uint4*>(x + (int64_t)m * K + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float xf[8];
+      widen(xq[m], xf);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float wf[8];
+        widen(wq[r], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r][m] = __builtin_fmaf(wf[e], xf[e], acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float v = acc[r][m];
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+      acc[r][m] = v;
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+        if (m < M && n0 + r < N) st(y, (int64_t)m * N + n0 + r, acc[r][m]);
+  }
+}
+
 template <typename F>
 int by_dtype(int dtype, F f) {
   switch (dtype) {
@@ -168,4 +228,32 @@ extern "C" int ssa_silu_mul(const void* gu, void* out, int32_t rows, int32_t I, 
                        static_cast<const T*>(gu), static_cast<T*>(out), (int64_t)rows, I);
     return (int)hipGetLastError();
   });
+}
+
+extern "C" int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
+                                 void* stream) {
+  if (!x || !W || !y || M < 1 || M > 8 || N < 1 || K < 8 || K % 8) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) return hipErrorInvalidValue;
+  if (dtype != kBF16 && dtype != kF16) return hipErrorInvalidValue;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto go = [&](auto tag, auto mm, auto rr) {
+    using T = decltype(tag);
+    constexpr int MM = decltype(mm)::value, R = decltype(rr)::value;
+    const int grid = (N + 4 * R - 1) / (4 * R);
+    hipLaunchKernelGGL((skinny_kernel<T, MM, R>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x),
+                       static_cast<const T*>(W), static_cast<T*>(y), M, N, K);
+    return (int)hipGetLastError();
+  };
+  // rows per wave: 4 when the columns give at least 1024 waves, else 1
+  auto pick = [&](auto tag, auto mm) {
+    if (N >= 4096) return go(tag, mm, std::integral_constant<int, 4>{});
+    return go(tag, mm, std::integral_constant<int, 1>{});
+  };
+  auto bym = [&](auto tag) {
+    if (M <= 1) return pick(tag, std::integral_constant<int, 1>{});
+    if (M <= 2) return pick(tag, std::integral_constant<int, 2>{});
+    if (M <= 4) return pick(tag, std::integral_constant<int, 4>{});
+    return pick(tag, std::integral_constant<int, 8>{});
+  };
+  return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
 }

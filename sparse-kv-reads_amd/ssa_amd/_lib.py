@@ -114,6 +114,7 @@ ENTRY_POINTS = {
     "ssa_qk_norm_rope_cache": (ct.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, ct.c_int32, ct.c_int32,
                                           ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32, vp]),
     "ssa_silu_mul": (ct.c_int, [vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
+    "ssa_linear_skinny": (ct.c_int, [vp, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
 }
 
 _lib = None

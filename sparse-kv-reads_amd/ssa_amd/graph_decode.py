@@ -14,8 +14,9 @@ Insertion: with insert-ahead (``SphereIndexGraph.insert_ahead``, chosen per laye
 ``prepare``) each layer's step launch bins its next key; otherwise one ``AllLayerInsert`` launch
 bins every layer's key at the start of the step, as the reference's ``fused_insert`` does.
 
-Glue: with ``glue="fused"`` (the default) each layer is four GEMMs (q/k/v, o, gate/up, down;
-the q/k/v and gate/up weights concatenated once), the attention step, and three HIP kernels
+Glue: with ``glue="fused"`` (the default) each layer is four projections (q/k/v, o, gate/up,
+down; the q/k/v and gate/up weights concatenated once; ``ssa_linear_skinny``, a weight-streaming
+kernel for the decode batch), the attention step, and three HIP kernels
 (``ssa_rmsnorm_add``: residual add + RMSNorm; ``ssa_qk_norm_rope_cache``: q/k RMSNorm, rotary
 embedding, KV-cache write; ``ssa_silu_mul``), instead of the ~60 element-wise launches of the
 model's own modules (``glue="torch"``, as the reference's ``_body`` runs them).
@@ -110,6 +111,17 @@ class GraphDecoder:
             return self.attn[i](qh, self._heads(kc), self._heads(vc), self.n_dev)
         return self.attn[i].step(qh, self._heads(kc), self._heads(vc), self.n_dev, insert=self.insert_all is None)
 
+    def _linear(self, x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
+        """``x W^T`` for the decode batch: the weight-streaming HIP kernel for 2-byte weights and
+        up to 8 rows, the library GEMM otherwise."""
+        M, K = x.shape
+        if M > 8 or W.dtype not in (torch.bfloat16, torch.float16) or K % 8:
+            return F.linear(x, W)
+        y = torch.empty(M, W.shape[0], device=x.device, dtype=x.dtype)
+        check(lib().ssa_linear_skinny(x.data_ptr(), W.data_ptr(), y.data_ptr(), M, W.shape[0], K, self._dt,
+                                      stream_ptr(x.device)), "ssa_linear_skinny")
+        return y
+
     def _body_fused(self) -> torch.Tensor:
         m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
         L, s, x, eps, dt = len(m.layers), stream_ptr(self.tok.device), self._x, self._eps, self._dt
@@ -121,7 +133,7 @@ class GraphDecoder:
                                     h.shape[1], eps, dt, s), "ssa_rmsnorm_add")
         for i, layer in enumerate(m.layers):
             a, f = layer.attn, layer.ffn
-            qkv = F.linear(x, self._wqkv[i])
+            qkv = self._linear(x, self._wqkv[i])
             kc, vc = self.cache.k[i], self.cache.v[i]
             check(lib().ssa_qk_norm_rope_cache(qkv.data_ptr(), a.q_norm.weight.data_ptr(), a.k_norm.weight.data_ptr(),
                                                m.rope_cos.data_ptr(), m.rope_sin.data_ptr(), self.pos.data_ptr(),
@@ -129,18 +141,18 @@ class GraphDecoder:
                                                kc.stride(1), kc.stride(2), B, H, H_kv, d, eps, dt, s),
                   "ssa_qk_norm_rope_cache")
             out = self._attend(i, self._qh, kc, vc)
-            o = F.linear(out.view(B, H * d), a.o.weight)
+            o = self._linear(out.view(B, H * d), a.o.weight)
             check(lib().ssa_rmsnorm_add(h.data_ptr(), o.data_ptr(), layer.norm2.weight.data_ptr(), x.data_ptr(), B,
                                         h.shape[1], eps, dt, s), "ssa_rmsnorm_add")
-            gu = F.linear(x, self._wgu[i])
+            gu = self._linear(x, self._wgu[i])
             check(lib().ssa_silu_mul(gu.data_ptr(), self._act.data_ptr(), B, self._act.shape[1], dt, s),
                   "ssa_silu_mul")
-            dn = F.linear(self._act, f.down.weight)
+            dn = self._linear(self._act, f.down.weight)
             nw = m.layers[i + 1].norm1.weight if i + 1 < L else m.final_norm.weight
             check(lib().ssa_rmsnorm_add(h.data_ptr(), dn.data_ptr(), nw.data_ptr(), x.data_ptr(), B, h.shape[1], eps,
                                         dt, s), "ssa_rmsnorm_add")
         head = m.embed.weight if m.lm_head is None else m.lm_head.weight
-        return F.linear(x, head).view(B, 1, -1)
+        return self._linear(x, head).view(B, 1, -1)
 
     def _body(self) -> torch.Tensor:
         if self.glue == "fused":

@@ -140,3 +140,19 @@ def test_fused_glue_matches_the_model_modules(dtype, tol):
     fused, _ = _graph_decode(model, ids, mode="dense", capture=True, glue="fused")
     ops, _ = _graph_decode(model, ids, mode="dense", capture=True, glue="torch")
     torch.testing.assert_close(fused, ops, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 1024), (2, 1024, 3072), (2, 6144, 1024), (5, 333, 264), (8, 64, 2048)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_skinny_linear_matches_an_fp32_product(M, N, K, dtype):
+    """The decode projections' weight-streaming kernel against an fp32 product of the same
+    operands: fp32 accumulation, one rounding."""
+    from ssa_amd._lib import check, dtype_tag, lib, stream_ptr
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + N)
+    x = torch.randn(M, K, device="cuda", generator=g).to(dtype)
+    W = (torch.randn(N, K, device="cuda", generator=g) * 0.05).to(dtype)
+    y = torch.empty(M, N, device="cuda", dtype=dtype)
+    check(lib().ssa_linear_skinny(x.data_ptr(), W.data_ptr(), y.data_ptr(), M, N, K, dtype_tag(dtype),
+                                  stream_ptr()), "ssa_linear_skinny")
+    want = (x.float() @ W.float().t().contiguous())
+    torch.testing.assert_close(y.float(), want, rtol=1e-2, atol=1e-2)
