@@ -190,9 +190,12 @@ def main() -> int:
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy 256 MiB device-to-device 5 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3, 4),
                     help="1: the headline workload; 2: the batched sweep of configs[2]; 3: whole-model Qwen3-0.6B "
-                         "decode of configs[3] (one JSON line each)")
+                         "decode of configs[3]; 4: Qwen3-4B long generation and batch-16 decode of configs[4] "
+                         "(one JSON line each)")
+    ap.add_argument("--long-prompt", type=int, default=8192, help="config 4: prompt of the long generation")
+    ap.add_argument("--long-total", type=int, default=32768, help="config 4: length the generation reaches")
     ap.add_argument("--tokens", type=int, default=1024, help="config 3: tokens generated per mode")
     ap.add_argument("--prompt", type=int, default=32768, help="config 3: prompt length per sequence")
     ap.add_argument("--batch", type=int, default=2, help="config 3: sequences")
@@ -224,6 +227,9 @@ def main() -> int:
         return 0
     if args.config == 3:
         print(json.dumps(model_decode(args, dev)), flush=True)
+        return 0
+    if args.config == 4:
+        print(json.dumps(model_long(args, dev)), flush=True)
         return 0
     global BUDGETS
     if args.budgets:
@@ -464,6 +470,118 @@ def model_decode(args, dev) -> dict:
             "config": {"workload": f"configs[3]: Qwen3-0.6B shape, batch {B}, prompt {P}, {Tn} tokens greedy",
                        "batch": B, "prompt": P, "tokens": Tn, "budgets": list(MODEL_BUDGETS)},
             "results": res}
+
+
+def _generate(dec, first, start, steps, *, probes=()):
+    """Greedy generation from ``first`` at positions start .. start+steps-1; returns the wall time of
+    the non-probe steps and {step: mean relative attention error over layers} at the probe steps."""
+    import torch
+    tok = first.clone()
+    errs, probe_s = {}, 0.0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        if k in probes:
+            torch.cuda.synchronize()
+            tp = time.perf_counter()
+            got = []
+            tok = dec.step(tok, start + k, probe=got)[:, -1].argmax(-1, keepdim=True)
+            errs[k] = round(float(torch.cat(got).mean()), 5)
+            torch.cuda.synchronize()
+            probe_s += time.perf_counter() - tp
+        else:
+            tok = dec.step(tok, start + k)[:, -1].argmax(-1, keepdim=True)
+        if k and k % 4096 == 0:
+            log(f"  step {k} of {steps}")
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0 - probe_s, errs
+
+
+def model_long(args, dev) -> dict:
+    """configs[4], Qwen3-4B shape (36 layers, hidden 2560, 32 q / 8 kv heads, d=128), random bf16
+    weights. (a) One sequence: a random ``long_prompt``-token prompt run through the model, then
+    greedy generation to ``long_total`` tokens with the clustered index (1,024 slots, 256 fitted at
+    the prompt, clusters split past 2x the prompt's mean cluster size, so the cluster count grows
+    with the context), and the same generation with dense attention; the relative error of every
+    layer's attention output against exact attention on the same query is probed at steps 1k, 8k
+    and 24k. (b) Batch 16 x 32k: synthetic caches (mixture-of-directions keys per layer, as
+    configs[1]; a 16 x 32k prefill through a 4B model is not part of the decode measurement), 64
+    decode steps per mode. Every step is one hipGraph replay."""
+    import torch
+    from ssa_amd.graph_decode import GraphDecoder
+    from ssa_amd.qwen3 import QWEN3_4B, random_model
+    from ssa_amd.synth import make_cache
+    cfg = QWEN3_4B
+    P, total = args.long_prompt, args.long_total
+    T = total - P
+    t0 = time.time()
+    model = random_model(cfg, dtype=torch.bfloat16, device=dev, seed=0)
+    ids = torch.randint(0, cfg.vocab_size, (1, P), device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+    base = model.alloc_cache(total + 1, batch=1)
+    with torch.inference_mode():
+        first = model(ids, base, start_pos=0, last_only=True)[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    log(f"config 4: model + prefill of {P} tokens in {time.time() - t0:.1f} s")
+    probes = tuple(k for k in (1000, 8000, 24000) if k < T)
+    long_res = {}
+    for mode in ("cluster", "dense"):
+        cache = model.alloc_cache(total + 1, batch=1)
+        for i in range(len(cache.k)):
+            cache.k[i].copy_(base.k[i])
+            cache.v[i].copy_(base.v[i])
+        cache.cur_len = P
+        with torch.inference_mode():
+            dec = GraphDecoder(model, cache, mode=mode, budget=0.2)
+            dec.prepare(P)
+            dec.capture()
+            wall, errs = _generate(dec, first, P, T, probes=probes if mode == "cluster" else ())
+        row = {"tokens_per_s": round((T - len(errs)) / wall, 1), "steps": T}
+        if mode == "cluster":
+            idx = dec.attn[0]
+            row.update({"attention_rel_error_at_step": errs, "clusters_layer0_end": round(float(idx.active_clusters), 1),
+                        "splits_layer0": int(idx.splits), "cap_layer0": round(float(idx.cap.float().mean()), 1)})
+        long_res[mode] = row
+        log(f"config 4 long {mode}: {json.dumps(row)}")
+        del dec, cache
+        torch.cuda.empty_cache()
+    long_res["cluster"]["speedup_vs_dense"] = round(long_res["cluster"]["tokens_per_s"] / long_res["dense"]["tokens_per_s"], 3)
+    del base
+    torch.cuda.empty_cache()
+    # (b) batch 16 x 32k
+    B, n, Tb = 16, 32768, 64
+    cache = model.alloc_cache(n + Tb + 9, batch=B)
+    for i in range(len(cache.k)):
+        K, V, _, _ = make_cache(B, cfg.num_key_value_heads, n + Tb + 9, cfg.head_dim, H=cfg.num_attention_heads,
+                                centers=C, capacity=n + Tb + 9, seed=500 + i, dtype=torch.bfloat16, device=dev,
+                                gen_device=str(dev))
+        cache.k[i].copy_(K)
+        cache.v[i].copy_(V)
+        del K, V
+    first = torch.randint(0, cfg.vocab_size, (B, 1), device=dev, generator=torch.Generator(device=dev).manual_seed(1))
+    log(f"config 4: batch {B} x {n} synthetic caches ready ({time.time() - t0:.0f} s)")
+    b16 = {}
+    for mode, budget in (("dense", None), ("cluster", 0.20), ("cluster", 0.05)):
+        cache.cur_len = n
+        with torch.inference_mode():
+            dec = GraphDecoder(model, cache, mode=mode, budget=budget or 0.2)
+            dec.prepare(n)
+            dec.capture()
+            _generate(dec, first, n, 8)
+            wall, _ = _generate(dec, first, n + 8, Tb)
+        key = "dense" if mode == "dense" else f"cluster_{int(budget * 100)}%"
+        b16[key] = {"tokens_per_s": round(B * Tb / wall, 1), "ms_per_step": round(wall / Tb * 1e3, 3)}
+        log(f"config 4 batch16 {key}: {json.dumps(b16[key])}")
+        del dec
+        torch.cuda.empty_cache()
+    for k in b16:
+        if k != "dense":
+            b16[k]["speedup_vs_dense"] = round(b16[k]["tokens_per_s"] / b16["dense"]["tokens_per_s"], 3)
+    return {"metric": "configs[4] Qwen3-4B long generation and batch-16 decode tokens/s (hipGraph step)",
+            "unit": "tokens/s", "higher_is_better": True, "n_gpus": 1, "dtype": "bf16",
+            "data": "random-init bf16 weights; random prompt ids (long run); synthetic KV caches (batch 16)",
+            "config": {"workload": f"configs[4]: Qwen3-4B shape, prompt {P} -> {total} greedy (budget 0.2), "
+                                   f"batch {B} x {n} decode", "budgets": [0.2, 0.05]},
+            "long_generation": long_res, "batch16_32k": b16}
 
 
 class _Shim:

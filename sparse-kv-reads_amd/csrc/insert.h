@@ -18,7 +18,7 @@ constexpr int kT = 256;       // threads per workgroup
 constexpr int kW = kT / 64;   // waves
 constexpr int kTile = 16;     // member rows of kMaxD staged in LDS by the split's ordered sums
 constexpr int kTileFloats = kTile * kMaxD;   // a tile holds kTileFloats / d rows of d
-constexpr int kGatherPer = 8; // label positions per thread per pass of the member scan
+constexpr int kGatherRun = 32;  // consecutive label positions per thread per pass of the member scan
 
 // LDS of the insertion and split code. A kernel that runs them passes a struct with the members
 // of InsertSmem (its own may add more to the union u, which must hold spl).
@@ -32,7 +32,6 @@ struct InsertBase {
   float va[kMaxD], vb[kMaxD], vs[kMaxD];
   float red_f[kW];
   int red_i[kW];
-  int gcnt[kGatherPer][kW];  // member scan: hits per (position slice, wave)
   float scal[4];
   int scali[4];
   float rmx, rmn;          // summaries of the cluster a key joins
@@ -331,49 +330,58 @@ __device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K,
 }
 
 // Positions of cluster c among [lo, hi), ascending, into H.mem[0 .. m) (at most H.ms); returns m.
-// Each pass scans kGatherPer * kT positions (position j0 + u * kT + tid for slice u), the next
-// pass's labels loading while this one is counted.
+// Each pass gives every thread kGatherRun consecutive positions (16-byte label loads where a
+// chunk of 8 lies inside [lo, hi), element loads at the two ends), the threads' runs in order;
+// an exclusive scan of the per-thread hit counts places every member.
 template <class SM>
 __device__ __forceinline__ int gather_members(SM& S, const Head& H, int c, int lo, int hi) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const unsigned long long below = (1ull << lane) - 1ull;
-  constexpr int PT = kGatherPer;
-  int lab[PT];
-  auto load = [&](int j0) {
-#pragma unroll
-    for (int u = 0; u < PT; ++u) {
-      const int j = j0 + u * kT + tid;
-      lab[u] = j < hi ? (int)H.labels[j] : -1;
-    }
-  };
+  if (lo >= hi) return 0;
+  // the row starts `mis` positions past a 16-byte boundary; a0 <= lo is the aligned start
+  const int mis = (int)((reinterpret_cast<uintptr_t>(H.labels) >> 1) & 7);
+  const int a0 = lo - ((lo + mis) & 7);
   int m = 0;
-  if (lo < hi) load(lo);
-  for (int j0 = lo; j0 < hi; j0 += PT * kT) {
-    bool hit[PT];
-    unsigned long long bal[PT];
+  for (int p0 = a0; p0 < hi; p0 += kT * kGatherRun) {
+    const int pb = p0 + tid * kGatherRun;
+    unsigned int bits = 0;
 #pragma unroll
-    for (int u = 0; u < PT; ++u) {
-      hit[u] = lab[u] == c;
-      bal[u] = __ballot(hit[u]);
-      if (lane == 0) S.gcnt[u][wave] = __popcll(bal[u]);
+    for (int q = 0; q < kGatherRun / 8; ++q) {
+      const int ps = pb + 8 * q;
+      int lab[8];
+      if (ps >= lo && ps + 8 <= hi) {
+        const uint4 r = *reinterpret_cast<const uint4*>(H.labels + ps);
+        const int16_t* v = reinterpret_cast<const int16_t*>(&r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lab[e] = v[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = ps + e;
+          lab[e] = (j >= lo && j < hi) ? (int)H.labels[j] : -1;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bits |= (lab[e] == c ? 1u : 0u) << (8 * q + e);
     }
-    if (j0 + PT * kT < hi) load(j0 + PT * kT);
+    const int cnt = __popc(bits);
+    const int incl = wave_incl_scan_dpp(cnt);
+    if (lane == 63) S.red_i[wave] = incl;
     __syncthreads();
+    int wb = 0, tot = 0;
 #pragma unroll
-    for (int u = 0; u < PT; ++u) {
-      int wb = 0, tot = 0;
-#pragma unroll
-      for (int w2 = 0; w2 < kW; ++w2) {
-        const int c2 = S.gcnt[u][w2];
-        if (w2 < wave) wb += c2;
-        tot += c2;
-      }
-      if (hit[u]) {
-        const int slot = m + wb + __popcll(bal[u] & below);
-        if (slot < H.ms) H.mem[slot] = j0 + u * kT + tid;
-      }
-      m += tot;
+    for (int w2 = 0; w2 < kW; ++w2) {
+      const int v = S.red_i[w2];
+      if (w2 < wave) wb += v;
+      tot += v;
     }
+    int slot = m + wb + incl - cnt;
+    while (bits) {
+      const int k = __ffs(bits) - 1;
+      bits &= bits - 1;
+      if (slot < H.ms) H.mem[slot] = pb + k;
+      ++slot;
+    }
+    m += tot;
     __syncthreads();
   }
   return min(m, H.ms);

@@ -76,6 +76,7 @@ class GraphDecoder:
                          for _ in model.layers]
         self.graph = None
         self.logits = None
+        self._probe = None
         self.fused_insert = fused_insert and mode == "cluster" and window >= 1
         self.insert_all = None
         if glue not in ("fused", "torch"):
@@ -109,7 +110,12 @@ class GraphDecoder:
     def _attend(self, i, qh, kc, vc):
         if self.mode == "dense":
             return self.attn[i](qh, self._heads(kc), self._heads(vc), self.n_dev)
-        return self.attn[i].step(qh, self._heads(kc), self._heads(vc), self.n_dev, insert=self.insert_all is None)
+        out = self.attn[i].step(qh, self._heads(kc), self._heads(vc), self.n_dev, insert=self.insert_all is None)
+        if self._probe is not None:                   # the exact output of the same query, for the error
+            from .labeled_attn import dense_attention
+            want = dense_attention(qh, self._heads(kc), self._heads(vc), n_dev=self.n_dev).float()
+            self._probe.append(((out.float() - want).norm() / want.norm().clamp_min(1e-30)).reshape(1))
+        return out
 
     def _linear(self, x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
         """``x W^T`` for the decode batch: the weight-streaming HIP kernel for 2-byte weights and
@@ -208,20 +214,31 @@ class GraphDecoder:
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self.logits = self._body()
+            self._glogits = self._body()
+        self.logits = self._glogits
         self.graph = g
         self._restore(snap)
         torch.cuda.synchronize()
 
-    def step(self, token: torch.Tensor, pos: int) -> torch.Tensor:
+    def step(self, token: torch.Tensor, pos: int, probe: list | None = None) -> torch.Tensor:
         """Decode ``token [B, 1]`` at position ``pos``; returns logits ``[B, 1, vocab]`` (a buffer
-        the next step overwrites)."""
+        the next step overwrites). With ``probe`` (cluster mode) the step runs eagerly, with the
+        same kernels as the graph, and appends for every layer the relative error
+        ``|out - dense| / |dense|`` of its attention output against exact attention on the same
+        query and cache (a one-element tensor per layer)."""
         if not 0 <= pos < self.cache.max_seq_len:
             raise ValueError("the cache is full")
         self.tok.copy_(token)
         self.pos.fill_(pos)
-        if self.graph is not None:
+        if probe is not None and self.mode == "cluster":
+            self._probe = probe
+            try:
+                self.logits = self._body()
+            finally:
+                self._probe = None
+        elif self.graph is not None:
             self.graph.replay()
+            self.logits = self._glogits
         else:
             self.logits = self._body()
         if self.mode == "cluster":
