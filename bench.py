@@ -194,6 +194,7 @@ def main() -> int:
                     help="1: the headline workload; 2: the batched sweep of configs[2]; 3: whole-model Qwen3-0.6B "
                          "decode of configs[3]; 4: Qwen3-4B long generation and batch-16 decode of configs[4] "
                          "(one JSON line each)")
+    ap.add_argument("--shapes", type=str, default="", help="config 2: comma list of BxN shapes (default: all)")
     ap.add_argument("--long-prompt", type=int, default=8192, help="config 4: prompt of the long generation")
     ap.add_argument("--long-total", type=int, default=32768, help="config 4: length the generation reaches")
     ap.add_argument("--tokens", type=int, default=1024, help="config 3: tokens generated per mode")
@@ -335,7 +336,10 @@ def batched_sweep(args, dev) -> dict:
     from ssa_amd.graph_kernels import DenseAttentionGraph, SphereIndexGraph
     from ssa_amd.synth import make_cache
     out = {}
-    for B, n in BATCHED:
+    shapes = BATCHED
+    if args.shapes:
+        shapes = tuple(tuple(int(v) for v in sh.split("x")) for sh in args.shapes.split(","))
+    for B, n in shapes:
         hk = B * H_KV
         kv_bytes = 2 * hk * n * D * 2
         rot = max(1, -(-(1 << 30) // kv_bytes))
