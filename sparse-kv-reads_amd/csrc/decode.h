@@ -55,7 +55,7 @@ struct DecodeParams {
 constexpr int kThreads = 256;
 static_assert(kThreads == kT, "the insertion code runs on the decode kernel's workgroup");
 constexpr int kWaves = kThreads / 64;
-constexpr int kPage = 1024;          // positions compacted per pass
+constexpr int kPage = 2048;          // positions compacted per pass
 constexpr int kMaxW = 1025;          // weight slots (C + 1) held in LDS per row
 
 template <int LPR>
@@ -272,13 +272,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
       if constexpr (DENSE) {
         R = pn;
       } else {
-        if (it > 0) {
-#pragma unroll
-          for (int u = 0; u < PER; ++u) {
-            const int j = block_pos(it, u) + tid;
-            lbl[u] = j < n ? (int)labrow[j] : 0;
-          }
-        }
+        // lbl holds this page's labels: the first page's were loaded at the start, each later
+        // page's while the previous page's rows were read
         __syncthreads();   // lw ready / previous page's list consumed
         // Position block_pos(it, u) + tid: the list in (u, wave, lane) order is ascending.
         bool sel[PER];
@@ -326,6 +321,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
           total += tot_u;
         }
         R = total;
+        // the next page's labels load while this page's rows are read
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const int j = block_pos(it + 1, u) + tid;
+          lbl[u] = j < n ? (int)labrow[j] : 0;
+        }
         __syncthreads();
       }
       rows_read += R;
