@@ -222,3 +222,28 @@ def test_end_to_end_config0_step():
     want = ref.label_weighted_attention(q.double().cpu().numpy(), K.double().cpu().numpy(),
                                         V.double().cpu().numpy(), canon.labels[:, :4096], want_w)
     np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("H,H_kv,d,dtype,group", [
+    (8, 8, 64, torch.float16, "sum_share"),      # G = 1
+    (32, 8, 128, torch.bfloat16, "sum_share"),   # G = 4 (Qwen3-4B)
+    (16, 2, 256, torch.bfloat16, "max"),         # G = 8, d = 256
+    (8, 4, 16, torch.float32, "per_head"),       # smallest head
+])
+def test_fused_step_shapes_match_the_oracle(H, H_kv, d, dtype, group):
+    """The fused step (selection in every workgroup, compaction, split-K attention, merge) at
+    the GQA groups, head sizes and cache dtypes the kernels are built for: selection bit-exact
+    against the oracle, output within the dtype's tolerance of the float64 spec."""
+    n = 2500
+    K, V, q = _keys(H_kv, n, d=d, H=H, seed=21, dtype=dtype, centers=32)
+    idx = _fused(C=64, window=16, delta=math.inf, check_every=10 ** 9)
+    out, labels, w = idx.attend(q, K, V, n=n, budget=0.2, group=group)
+    torch.cuda.synchronize()
+    canon = _canon_like(idx, K, n)
+    _same(idx, canon)
+    want_w = canon.select(q, budget=0.2, group=group)
+    assert np.array_equal(w.cpu().numpy(), want_w)
+    want = ref.label_weighted_attention(q.double().cpu().numpy(), K.double().cpu().numpy(),
+                                        V.double().cpu().numpy(), canon.labels[:, :n], want_w)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=tol)
