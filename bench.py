@@ -160,10 +160,24 @@ def cpu_baseline(seconds: float):
         rows = [int((w[h][labels[h].astype(np.int64)] > 0).sum()) for h in range(H_KV)]
     times.sort()
     med = times[len(times) // 2]
+    # configs[0] exactly: n = 4096, the same path, 20 steps
+    n0 = 4096
+    K0, V0, q0, _ = make_cache(1, H_KV, n0 + 32, D, H=H, centers=C, seed=0, dtype=torch.float32)
+    K0, V0, q0 = K0[0].numpy(), V0[0].numpy(), q0[0].numpy()
+    ref0 = SphereIndexRef(C=C, window=WINDOW, init_indices=lambda m, c, s: kmeans_init_indices(m, c, s).numpy())
+    ref0.observe(K0, n0)
+    t0s = []
+    for k in range(1, 21):
+        t = time.time()
+        ref0.attend(q0, K0, V0, n=n0 + k, budget=HEADLINE, fast=True)
+        t0s.append(time.time() - t)
+    t0s.sort()
     return {"value": step_bytes(rows, n) / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "us_per_step": med * 1e6, "prefill_s": prefill,
+            "config0_us_per_step": t0s[len(t0s) // 2] * 1e6,
             "sample": f"{len(times)} decode steps at n={N}..{n}, fp32, B=1, 16/8 heads, d=128, C=256, "
-                      f"budget {HEADLINE}, after one k-means prefill ({prefill:.1f} s); median step",
+                      f"budget {HEADLINE}, after one k-means prefill ({prefill:.1f} s); median step "
+                      f"(config0_us_per_step: the same path at configs[0], n=4096, median of 20 steps)",
             "cpu": _cpu_model()}
 
 
