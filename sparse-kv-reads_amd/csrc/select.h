@@ -519,12 +519,14 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
   if (group == 0) {
     // sum_share: per head a softmax over live clusters, summed over the heads
     float t[KPT][GMAX];
+    const int kact = min(C, n_act);             // rounds past the slots in use hold no live cluster
 #pragma unroll
     for (int k = 0; k < KPT; ++k) {
       const int c = sel_slot(tid, k);
 #pragma unroll
       for (int g = 0; g < GMAX; ++g) {
-        t[k][g] = (cnt[k] > 0 && g < G) ? cexp(z[k][g] - zmx[g]) : 0.f;
+        t[k][g] = 0.f;
+        if (256 * k < kact && cnt[k] > 0 && g < G) t[k][g] = cexp(z[k][g] - zmx[g]);
         if (g < G && c < C) S.z[g][c] = t[k][g];
       }
     }
@@ -556,11 +558,14 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < KPT; ++k) {
-      float s = 0.f;
+      key[k] = -INFINITY;
+      if (256 * k < kact && cnt[k] > 0) {
+        float s = 0.f;
 #pragma unroll
-      for (int g = 0; g < GMAX; ++g)
-        if (g < G) s = s + t[k][g] / S.tree[g];
-      key[k] = cnt[k] > 0 ? s : -INFINITY;
+        for (int g = 0; g < GMAX; ++g)
+          if (g < G) s = s + t[k][g] / S.tree[g];
+        key[k] = s;
+      }
     }
   } else {
     // max / max_rel
