@@ -55,7 +55,9 @@ struct DecodeParams {
 constexpr int kThreads = 256;
 static_assert(kThreads == kT, "the insertion code runs on the decode kernel's workgroup");
 constexpr int kWaves = kThreads / 64;
-constexpr int kPage = 2048;          // positions compacted per pass
+// positions compacted per pass: the selected-row list (position + GMAX weights per row) lives in
+// LDS, so the page shrinks as the weight rows grow
+template <int GMAX> constexpr int page_size() { return GMAX <= 4 ? 2048 : 1024; }
 constexpr int kMaxW = 1025;          // weight slots (C + 1) held in LDS per row
 
 template <int LPR>
@@ -114,12 +116,13 @@ __device__ __forceinline__ float load_coherent(const float* p) {
 
 template <int D, int GMAX, bool DENSE>
 struct DecodeSmem {
+  static constexpr int kPage = page_size<GMAX>();
   static constexpr int kSelG = DENSE ? 1 : GMAX;
   float lw[DENSE ? 1 : GMAX][DENSE ? 1 : kMaxW];       // log2 w per weight row, -inf where w <= 0
   union {
     struct {
-      int pos[kPage];                                    // selected positions of the current page
-      float rlw[GMAX][kPage];                            // their log2 w per weight row
+      int pos[DENSE ? 1 : kPage];                        // selected positions of the current page
+      float rlw[GMAX][DENSE ? 1 : kPage];                // their log2 w per weight row
     } list;
     SelSmem<kSelG> sel;                                  // fused selection scratch
     InsertSmem tail;                                     // fused insertion ahead
@@ -145,6 +148,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   constexpr int LPR = D / 8;           // lanes per row
   constexpr int RPI = 64 / LPR;        // rows per wave instruction
   constexpr int U = kRowsInFlight;     // rows in flight per lane group
+  constexpr int kPage = page_size<GMAX>();
   constexpr int PER = kPage / kThreads;
   using Raw = typename RawRow<T>::type;
   __shared__ DecodeSmem<D, GMAX, DENSE> sm;
