@@ -200,3 +200,25 @@ def test_dense_attention_host_and_device_length(dtype, atol):
     dag = DenseAttentionGraph(H=16, H_kv=H_KV, d=D, dtype=dtype, device=q.device)
     got2 = dag(q, K, V, torch.tensor([n], dtype=torch.int32, device="cuda"))
     np.testing.assert_allclose(_np(got2), want, rtol=0, atol=atol)
+
+
+@pytest.mark.parametrize("field,value", [("G", 0), ("G", 9), ("S", 0), ("S", 257), ("n_heads", 0), ("d", 48),
+                                         ("w_len", 0), ("w_len", 1026)])
+def test_bad_arguments_are_refused_before_any_launch(field, value):
+    """The C ABI checks its scalar arguments and returns hipErrorInvalidValue (1) without
+    launching: GQA group 1..8, splits 1..256, head size 16/32/64/128/256, weight slots 1..1025."""
+    from ssa_amd._lib import lib, stream_ptr
+    from ssa_amd.labeled_attn import SplitWork, attn_args
+    q, K, V, labels = _inputs(300)
+    w = torch.ones(H_KV, L, device="cuda")
+    work = SplitWork(H_KV, 4, H // H_KV, D, q.device)
+    out = torch.empty_like(q)
+    a = attn_args(q, K, V, out, work, labels=labels, w=w, n_host=300)
+    setattr(a, field, value)
+    rc = lib().ssa_label_attention(a, stream_ptr(q.device))
+    torch.cuda.synchronize()
+    assert rc == 1
+    # the same arguments with the field restored still work
+    a = attn_args(q, K, V, out, work, labels=labels, w=w, n_host=300)
+    assert lib().ssa_label_attention(a, stream_ptr(q.device)) == 0
+    torch.cuda.synchronize()
