@@ -450,21 +450,21 @@ def model_decode(args, dev) -> dict:
         cache.cur_len = P
         t1 = time.time()
         with torch.inference_mode():
-            dec = GraphDecoder(model, cache, mode=mode, budget=budget or 0.2)
+            dec = GraphDecoder(model, cache, mode=mode, budget=budget or 0.2, greedy=True)
             dec.prepare(P)
             dec.capture()
         torch.cuda.synchronize()
         prep = time.time() - t1
         tok = first.clone()
-        toks = []
         with torch.inference_mode():
             for pos in range(P, P + 8):                                    # warm-up steps, not timed
-                tok = dec.step(tok, pos)[:, -1].argmax(-1, keepdim=True)
+                dec.step(tok, pos)
+                tok = dec.next_tok                                          # the greedy token, in the graph
             torch.cuda.synchronize()
             t2 = time.perf_counter()
             for pos in range(P + 8, P + Tn):
-                tok = dec.step(tok, pos)[:, -1].argmax(-1, keepdim=True)
-                toks.append(tok)
+                dec.step(tok, pos)
+                tok = dec.next_tok
             torch.cuda.synchronize()
             wall = time.perf_counter() - t2
         steps = Tn - 8
@@ -503,12 +503,14 @@ def _generate(dec, first, start, steps, *, probes=()):
             torch.cuda.synchronize()
             tp = time.perf_counter()
             got = []
-            tok = dec.step(tok, start + k, probe=got)[:, -1].argmax(-1, keepdim=True)
+            dec.step(tok, start + k, probe=got)
+            tok = dec.next_tok
             errs[k] = round(float(torch.cat(got).mean()), 5)
             torch.cuda.synchronize()
             probe_s += time.perf_counter() - tp
         else:
-            tok = dec.step(tok, start + k)[:, -1].argmax(-1, keepdim=True)
+            dec.step(tok, start + k)
+            tok = dec.next_tok
         if k and k % 4096 == 0:
             log(f"  step {k} of {steps}")
     torch.cuda.synchronize()
@@ -549,7 +551,7 @@ def model_long(args, dev) -> dict:
             cache.v[i].copy_(base.v[i])
         cache.cur_len = P
         with torch.inference_mode():
-            dec = GraphDecoder(model, cache, mode=mode, budget=0.2)
+            dec = GraphDecoder(model, cache, mode=mode, budget=0.2, greedy=True)
             dec.prepare(P)
             dec.capture()
             wall, errs = _generate(dec, first, P, T, probes=probes if mode == "cluster" else ())
@@ -581,7 +583,7 @@ def model_long(args, dev) -> dict:
     for mode, budget in (("dense", None), ("cluster", 0.20), ("cluster", 0.05)):
         cache.cur_len = n
         with torch.inference_mode():
-            dec = GraphDecoder(model, cache, mode=mode, budget=budget or 0.2)
+            dec = GraphDecoder(model, cache, mode=mode, budget=budget or 0.2, greedy=True)
             dec.prepare(n)
             dec.capture()
             _generate(dec, first, n, 8)

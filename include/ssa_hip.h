@@ -232,6 +232,9 @@ int ssa_silu_mul(const void* gu, void* out, int32_t rows, int32_t I, int32_t dty
 int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
                       void* stream);
 
+/* out [M] int64 = the index of the first maximum of each row of x [M, N] (greedy decoding). */
+int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

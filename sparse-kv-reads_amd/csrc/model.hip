@@ -257,3 +257,41 @@ extern "C" int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t 
   };
   return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
 }
+
+// out [M] int64 = argmax over each row of x [M, N] (first index of the maximum), one workgroup of
+// 1024 threads per row.
+template <typename T>
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out, int N) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int64_t row = (int64_t)blockIdx.x * N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float bv = -INFINITY;
+  int bi = N;
+  for (int i = tid; i < N; i += 1024) {
+    const float v = ld(x, row + i);
+    if (v > bv || (v == bv && i < bi) || (v != v && bi == N)) { bv = v; bi = i; }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(bv, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    if (v2 > bv || (v2 == bv && i2 < bi)) { bv = v2; bi = i2; }
+  }
+  if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
+    out[blockIdx.x] = bi < N ? bi : 0;
+  }
+}
+
+extern "C" int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t dtype, void* stream) {
+  if (!x || !out || M < 1 || N < 1) return hipErrorInvalidValue;
+  return by_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL(argmax_rows_kernel<T>, dim3(M), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<const T*>(x), out, N);
+    return (int)hipGetLastError();
+  });
+}

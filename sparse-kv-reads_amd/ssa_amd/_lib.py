@@ -115,6 +115,7 @@ ENTRY_POINTS = {
                                           ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32, vp]),
     "ssa_silu_mul": (ct.c_int, [vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
     "ssa_linear_skinny": (ct.c_int, [vp, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
+    "ssa_argmax_rows": (ct.c_int, [vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
 }
 
 _lib = None

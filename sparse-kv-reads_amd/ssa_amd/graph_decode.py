@@ -40,7 +40,7 @@ class GraphDecoder:
                  C_init: int | None = None, split_factor: float | None = None, refit_every: int = 0,
                  grow_cap: bool = False, reset_at: int = 0, summary_bits: int = 8, cap_keys: float = 0.0,
                  fused_insert: bool = True, var_factor: float = 0.0, var_min: int = 8,
-                 insert_ahead: bool | None = None, glue: str = "fused", **_):
+                 insert_ahead: bool | None = None, glue: str = "fused", greedy: bool = False, **_):
         cfg = model.cfg
         # with no slot count given: 1,024 slots, 256 clusters fitted at the prompt, splitting of
         # clusters over twice the mean size at the fit (src/ssa/models/graph_decode.py:35-43)
@@ -77,6 +77,8 @@ class GraphDecoder:
         self.graph = None
         self.logits = None
         self._probe = None
+        self.greedy = greedy
+        self.next_tok = torch.zeros(B, 1, dtype=torch.long, device=dev)   # with greedy: argmax of the logits
         self.fused_insert = fused_insert and mode == "cluster" and window >= 1
         self.insert_all = None
         if glue not in ("fused", "torch"):
@@ -158,7 +160,11 @@ class GraphDecoder:
             check(lib().ssa_rmsnorm_add(h.data_ptr(), dn.data_ptr(), nw.data_ptr(), x.data_ptr(), B, h.shape[1], eps,
                                         dt, s), "ssa_rmsnorm_add")
         head = m.embed.weight if m.lm_head is None else m.lm_head.weight
-        return self._linear(x, head).view(B, 1, -1)
+        logits = self._linear(x, head)
+        if self.greedy:
+            check(lib().ssa_argmax_rows(logits.data_ptr(), self.next_tok.data_ptr(), B, logits.shape[1], dt, s),
+                  "ssa_argmax_rows")
+        return logits.view(B, 1, -1)
 
     def _body(self) -> torch.Tensor:
         if self.glue == "fused":
@@ -184,7 +190,10 @@ class GraphDecoder:
             out = self._attend(i, qh, kc, vc)
             h = h + a.o(out.reshape(B, 1, H * d))
             h = h + layer.ffn(layer.norm2(h))
-        return m.logits(h)
+        logits = m.logits(h)
+        if self.greedy:
+            self.next_tok.copy_(logits[:, -1].argmax(-1, keepdim=True))
+        return logits
 
     def _snapshot(self):
         """Copies of every index state tensor (the capture's warm-up runs execute real steps)."""

@@ -156,3 +156,21 @@ def test_skinny_linear_matches_an_fp32_product(M, N, K, dtype):
                                   stream_ptr()), "ssa_linear_skinny")
     want = (x.float() @ W.float().t().contiguous())
     torch.testing.assert_close(y.float(), want, rtol=1e-2, atol=1e-2)
+
+
+def test_greedy_token_is_the_argmax_of_the_logits():
+    """With ``greedy`` the captured step also writes the argmax of its logits (first maximum)."""
+    model, _ = _setup(torch.bfloat16)
+    cache = model.alloc_cache(P + T + 1, batch=2)
+    ids = torch.randint(0, CFG.vocab_size, (2, P), device="cuda", generator=torch.Generator(device="cuda").manual_seed(4))
+    with torch.inference_mode():
+        model(ids, cache, start_pos=0, last_only=True)
+        dec = GraphDecoder(model, cache, mode="cluster", budget=0.2, C=16, window=4, greedy=True)
+        dec.prepare(P)
+        dec.capture()
+        tok = ids[:, -1:]
+        for pos in range(P, P + 6):
+            lg = dec.step(tok, pos)
+            torch.cuda.synchronize()
+            assert torch.equal(dec.next_tok, lg[:, -1].argmax(-1, keepdim=True)), pos
+            tok = dec.next_tok.clone()
