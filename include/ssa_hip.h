@@ -232,8 +232,23 @@ int ssa_silu_mul(const void* gu, void* out, int32_t rows, int32_t I, int32_t dty
 int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
                       void* stream);
 
-/* out [M] int64 = the index of the first maximum of each row of x [M, N] (greedy decoding). */
-int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t dtype, void* stream);
+/* out [M] int64 = the index of the first maximum of each row of x [M, N], a NaN counting as
+ * above every number (greedy decoding). work: 12 M bytes of device memory, 8-byte aligned, zero
+ * before the first call; every call leaves it zero. Calls that share a work buffer must not run
+ * at the same time. */
+int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t dtype, void* work, void* stream);
+
+/* act [M, I] = round(silu(g)) * u, (g, u) = x [M, K] W [2 I, K]^T rounded to the dtype (W holds
+ * the gate rows, then the up rows): ssa_linear_skinny followed by ssa_silu_mul in one launch,
+ * with the same bits. Same limits as ssa_linear_skinny. */
+int ssa_linear_swiglu(const void* x, const void* W, void* act, int32_t M, int32_t I, int32_t K, int32_t dtype,
+                      void* stream);
+
+/* h [rows, D] = embed [vocab, D] row tok[r] (int64, clamped to the table), then x = RMSNorm(h) * w
+ * as ssa_rmsnorm_add without delta; if n_out, *n_out = *pos + 1 (int32, the step's cache length):
+ * the first launch of a decode step. */
+int ssa_embed_rmsnorm(const int64_t* tok, const void* embed, void* h, const void* w, void* x, int32_t rows, int32_t D,
+                      int64_t vocab, float eps, const int64_t* pos, int32_t* n_out, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

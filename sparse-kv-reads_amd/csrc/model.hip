@@ -53,10 +53,48 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(T* __restrict__ h, con
   }
 }
 
+// One query or key head of d entries (entry i read as load(i)): RMSNorm over d with weight w,
+// then the rotary embedding at pos, stored to dst. One wave; lane t owns pairs (t + 64 u,
+// t + 64 u + d/2).
+template <typename T, typename F>
+__device__ __forceinline__ void norm_rope_store(F load, const T* __restrict__ w, const float* __restrict__ cos_t,
+                                                const float* __restrict__ sin_t, int64_t pos, T* __restrict__ dst,
+                                                int d, float eps, int lane) {
+  constexpr int kMaxPairs = 2;                      // d <= 256
+  const int half = d / 2;
+  // every input is loaded before the first use, in one round of loads
+  float x1[kMaxPairs], x2[kMaxPairs], w1[kMaxPairs], w2[kMaxPairs], co[kMaxPairs], si[kMaxPairs];
+#pragma unroll
+  for (int u = 0; u < kMaxPairs; ++u) {
+    const int i = lane + 64 * u;
+    const bool ok = i < half;
+    x1[u] = ok ? load(i) : 0.f;
+    x2[u] = ok ? load(i + half) : 0.f;
+    w1[u] = ok ? ld(w, i) : 0.f;
+    w2[u] = ok ? ld(w, i + half) : 0.f;
+    co[u] = ok ? cos_t[pos * half + i] : 0.f;
+    si[u] = ok ? sin_t[pos * half + i] : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < kMaxPairs; ++u) ss += x1[u] * x1[u] + x2[u] * x2[u];
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)d + eps);
+#pragma unroll
+  for (int u = 0; u < kMaxPairs; ++u) {
+    const int i = lane + 64 * u;
+    if (i >= half) continue;
+    const float a = rnd<T>((x1[u] * r) * w1[u]);
+    const float c = rnd<T>((x2[u] * r) * w2[u]);
+    st(dst, i, a * co[u] - c * si[u]);
+    st(dst, i + half, c * co[u] + a * si[u]);
+  }
+}
+
 // qkv [B, (H + 2 Hk) d]: head slot j of sequence b is a query head (j < H), a key head
 // (j < H + Hk) or a value head. Queries and keys: RMSNorm over d with their weight, then the
 // rotary embedding at *pos; queries go to q_out [B H, d], keys to the cache at *pos, values are
-// copied to the cache. One wave per (head slot, sequence); lane t owns pairs (t + 64 u, .. + d/2).
+// copied to the cache. One wave per (head slot, sequence).
 template <typename T>
 __global__ __launch_bounds__(64) void qk_norm_rope_cache_kernel(const T* __restrict__ qkv, const T* __restrict__ qw,
                                                                 const T* __restrict__ kw, const float* __restrict__ cos_t,
@@ -65,8 +103,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_cache_kernel(const T* __restr
                                                                 T* __restrict__ kc, T* __restrict__ vc, int64_t s_cb,
                                                                 int64_t s_ch, int64_t s_cl, int H, int Hk, int d,
                                                                 float eps) {
-  constexpr int kMaxPairs = 2;                      // d <= 256
-  const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x, half = d / 2;
+  const int j = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int64_t pos = *pos_p;
   const T* src = qkv + ((int64_t)b * (H + 2 * Hk) + j) * d;
   if (j >= H + Hk) {                                // value head: copy into the cache
@@ -75,29 +112,8 @@ __global__ __launch_bounds__(64) void qk_norm_rope_cache_kernel(const T* __restr
     return;
   }
   const bool is_q = j < H;
-  const T* w = is_q ? qw : kw;
-  float x1[kMaxPairs], x2[kMaxPairs];
-  float ss = 0.f;
-#pragma unroll
-  for (int u = 0; u < kMaxPairs; ++u) {
-    const int i = lane + 64 * u;
-    x1[u] = i < half ? ld(src, i) : 0.f;
-    x2[u] = i < half ? ld(src, i + half) : 0.f;
-    ss += x1[u] * x1[u] + x2[u] * x2[u];
-  }
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss / (float)d + eps);
   T* dst = is_q ? q_out + ((int64_t)b * H + j) * d : kc + b * s_cb + (int64_t)(j - H) * s_ch + pos * s_cl;
-#pragma unroll
-  for (int u = 0; u < kMaxPairs; ++u) {
-    const int i = lane + 64 * u;
-    if (i >= half) continue;
-    const float a = rnd<T>((x1[u] * r) * ld(w, i));
-    const float c = rnd<T>((x2[u] * r) * ld(w, i + half));
-    const float co = cos_t[pos * half + i], si = sin_t[pos * half + i];
-    st(dst, i, a * co - c * si);
-    st(dst, i + half, c * co + a * si);
-  }
+  norm_rope_store<T>([&](int i) { return ld(src, i); }, is_q ? qw : kw, cos_t, sin_t, pos, dst, d, eps, lane);
 }
 
 // out [rows, I] = round(silu(gate)) * up, gu [rows, 2 I] holding gate then up
@@ -113,18 +129,15 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu,
   }
 }
 
-// y [M, N] = x [M, K] . W[N, K]^T for a handful of rows M (decode batch): a weight-streaming
-// kernel. Wave w of workgroup b owns output columns n0 = (4 b + w) R .. n0 + R; every lane
-// reads 16 bytes (8 elements) of each of the R weight rows per k-step of 512 elements and dots
-// them with the matching 8 elements of the M rows of x (fp32 accumulation), then the 64 lane
-// partials are summed by a shuffle tree and rounded once to the output dtype.
-template <typename T, int MM, int R>
-__global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, const T* __restrict__ W,
-                                                     T* __restrict__ y, int M, int N, int K) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * 4 + wave) * R;
-  if (n0 >= N) return;
-  float acc[R][MM];
+// The weight-streaming products of the decode step (a handful of rows M, the decode batch).
+// A wave owns R weight rows; every lane reads 16 bytes (8 elements) of each of them per k-step
+// of 512 elements and dots them with the matching 8 elements of the M rows of x in fp32, then the
+// 64 lane partials are summed by a shuffle tree. Every kernel below uses these two functions, so
+// an output column has the same bits whichever kernel computes it.
+// row(r): the weight row of slot r, or -1 for none (its sums stay 0).
+template <typename T, int MM, int R, typename RowFn>
+__device__ __forceinline__ void skinny_dots(const T* __restrict__ x, const T* __restrict__ W, int M, int K, int lane,
+                                            RowFn row, float (&acc)[R][MM]) {
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -134,12 +147,15 @@ __global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, co
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = to_f32(h[e]);
   };
+  int64_t rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rows[r] = row(r);
 #pragma unroll 2
   for (int k0 = 8 * lane; k0 < K; k0 += 512) {
     uint4 wq[R], xq[MM];
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      wq[r] = n0 + r < N ? *reinterpret_cast<const uint4*>(W + (int64_t)(n0 + r) * K + k0) : make_uint4(0, 0, 0, 0);
+      wq[r] = rows[r] >= 0 ? *reinterpret_cast<const uint4*>(W + rows[r] * K + k0) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int m = 0; m < MM; ++m)
       xq[m] = m < M ? *reinterpret_cast<const uint4*>(x + (int64_t)m * K + k0) : make_uint4(0, 0, 0, 0);
@@ -164,12 +180,81 @@ __global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, co
       for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
       acc[r][m] = v;
     }
+}
+
+// y [M, N] = x [M, K] . W[N, K]^T, rounded once to the output dtype. Wave w of workgroup b owns
+// output columns n0 = (4 b + w) R .. n0 + R.
+template <typename T, int MM, int R>
+__global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, const T* __restrict__ W,
+                                                     T* __restrict__ y, int M, int N, int K) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * R;
+  if (n0 >= N) return;
+  float acc[R][MM];
+  skinny_dots<T, MM, R>(x, W, M, K, lane, [&](int r) { return n0 + r < N ? (int64_t)(n0 + r) : (int64_t)-1; }, acc);
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < MM; ++m)
         if (m < M && n0 + r < N) st(y, (int64_t)m * N + n0 + r, acc[r][m]);
+  }
+}
+
+// act [M, I] = round(silu(g)) * u with (g, u) = x . W[2 I, K]^T rounded to the dtype (gate rows
+// first, then up rows): the gate/up projection with the SwiGLU activation as its epilogue, equal
+// bit for bit to ssa_linear_skinny followed by ssa_silu_mul. Wave w of workgroup b owns
+// activation columns c0 = 2 (4 b + w), c0 + 1: weight rows c0, c0 + 1, I + c0, I + c0 + 1.
+template <typename T, int MM>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ x, const T* __restrict__ W,
+                                                     T* __restrict__ act, int M, int I, int K) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c0 = (blockIdx.x * 4 + wave) * 2;
+  if (c0 >= I) return;
+  float acc[4][MM];
+  skinny_dots<T, MM, 4>(x, W, M, K, lane, [&](int r) {
+    const int c = c0 + (r & 1);
+    return c < I ? (int64_t)((r < 2 ? 0 : I) + c) : (int64_t)-1;
+  }, acc);
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+        if (m < M && c0 + q < I) {
+          const float g = rnd<T>(acc[q][m]), u = rnd<T>(acc[2 + q][m]);
+          const float sl = rnd<T>(g / (1.0f + expf(-g)));
+          st(act, (int64_t)m * I + c0 + q, sl * u);
+        }
+  }
+}
+
+// h [rows, D] = embed[tok[row]], x = rmsnorm(h) * w (as ssa_rmsnorm_add without delta), and
+// *n_out = *pos + 1 (the step's cache length): the first glue of a decode step.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_rmsnorm_kernel(const int64_t* __restrict__ tok, const T* __restrict__ emb,
+                                                            T* __restrict__ h, const T* __restrict__ w,
+                                                            T* __restrict__ x, int D, int64_t vocab, float eps,
+                                                            const int64_t* __restrict__ pos, int32_t* __restrict__ n_out) {
+  __shared__ float red[4];
+  const int64_t row = (int64_t)blockIdx.x * D;
+  const int tid = threadIdx.x;
+  const int64_t t = min(max(tok[blockIdx.x], (int64_t)0), vocab - 1);
+  if (blockIdx.x == 0 && tid == 0 && n_out) *n_out = (int32_t)(*pos + 1);
+  float ss = 0.f;
+  for (int i = tid; i < D; i += 256) {
+    const T e = emb[t * D + i];
+    h[row + i] = e;
+    const float v = to_f32(e);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float r = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+  for (int i = tid; i < D; i += 256) {
+    const float v = to_f32(emb[t * D + i]);
+    st(x, row + i, (v * r) * ld(w, i));
   }
 }
 
@@ -258,40 +343,140 @@ extern "C" int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t 
   return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
 }
 
-// out [M] int64 = argmax over each row of x [M, N] (first index of the maximum), one workgroup of
-// 1024 threads per row.
+// out [M] int64 = argmax over each row of x [M, N]: the first index of the maximum, a NaN counting
+// as above every number (torch.argmax's rule). Grid (P, M): workgroup p scans the p-th of P
+// slices of a row (16-byte loads of 8 elements when the dtype is 2 bytes, N a multiple of 8 and
+// the rows 16-byte aligned), reduces to one (value, index) and folds it into the row's 64-bit key
+// with an agent-scope atomic max; the key orders as arg_better does. The last workgroup of the row
+// to count itself in writes the index and returns key and count to zero for the next call.
+constexpr int kArgThreads = 256, kArgMaxParts = 64, kArgSlice = 2048;
+__device__ __forceinline__ bool arg_better(float v2, int i2, float v1, int i1) {
+  if (v2 != v2) return v1 == v1 || i2 < i1;
+  if (v1 != v1) return false;
+  return v2 > v1 || (v2 == v1 && i2 < i1);
+}
+// unsigned order of the key = arg_better's order: value bits made monotone (NaN above +inf, -0 as
+// +0) above the complemented index
+__device__ __forceinline__ unsigned long long arg_key(float v, int i) {
+  unsigned int b;
+  if (v != v) {
+    b = 0xffffffffu;
+  } else {
+    const unsigned int f = __float_as_uint(v + 0.0f);
+    b = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+  }
+  return ((unsigned long long)b << 32) | (unsigned long long)(~(unsigned int)i);
+}
+
 template <typename T>
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out, int N) {
-  __shared__ float sv[16];
-  __shared__ int si[16];
-  const int64_t row = (int64_t)blockIdx.x * N;
+__global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const T* __restrict__ x, int64_t* __restrict__ out,
+                                                                  int N, int vec, unsigned long long* __restrict__ key,
+                                                                  unsigned int* __restrict__ cnt) {
+  __shared__ float sv[kArgThreads / 64];
+  __shared__ int si[kArgThreads / 64];
+  const int r = blockIdx.y, P = gridDim.x, p = blockIdx.x;
+  const T* row = x + (int64_t)r * N;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float bv = -INFINITY;
   int bi = N;
-  for (int i = tid; i < N; i += 1024) {
-    const float v = ld(x, row + i);
-    if (v > bv || (v == bv && i < bi) || (v != v && bi == N)) { bv = v; bi = i; }
+  const int units = vec ? N / 8 : N;                 // 8-element chunks or elements
+  const int per = (units + P - 1) / P;
+  const int u0 = min(p * per, units), u1 = min(u0 + per, units);
+  if (vec) {
+    const uint4* rv = reinterpret_cast<const uint4*>(row);
+    for (int c0 = u0 + tid; c0 < u1; c0 += 4 * kArgThreads) {
+      uint4 q[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = c0 + k * kArgThreads;
+        q[k] = c < u1 ? rv[c] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = c0 + k * kArgThreads;
+        if (c >= u1) break;
+        const T* e = reinterpret_cast<const T*>(&q[k]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float v = to_f32(e[t]);
+          if (arg_better(v, 8 * c + t, bv, bi)) { bv = v; bi = 8 * c + t; }
+        }
+      }
+    }
+  } else {
+    for (int i = u0 + tid; i < u1; i += kArgThreads) {
+      const float v = ld(row, i);
+      if (arg_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     const float v2 = __shfl_xor(bv, o, 64);
     const int i2 = __shfl_xor(bi, o, 64);
-    if (v2 > bv || (v2 == bv && i2 < bi)) { bv = v2; bi = i2; }
+    if (arg_better(v2, i2, bv, bi)) { bv = v2; bi = i2; }
   }
   if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
   __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < 16; ++w)
-      if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-    out[blockIdx.x] = bi < N ? bi : 0;
-  }
+  if (tid != 0) return;
+  for (int w = 1; w < kArgThreads / 64; ++w)
+    if (arg_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+  // the returning max completes at the coherence point before this workgroup counts itself in
+  if (bi < N) (void)__hip_atomic_fetch_max(key + r, arg_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned int old = __hip_atomic_fetch_add(cnt + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old != (unsigned int)(P - 1)) return;
+  const unsigned long long k = __hip_atomic_load(key + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  out[r] = (int64_t)(~(unsigned int)(k & 0xffffffffull));
+  __hip_atomic_store(key + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(cnt + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-extern "C" int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t dtype, void* stream) {
-  if (!x || !out || M < 1 || N < 1) return hipErrorInvalidValue;
+extern "C" int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t dtype, void* work,
+                               void* stream) {
+  if (!x || !out || !work || M < 1 || N < 1) return hipErrorInvalidValue;
+  if (reinterpret_cast<uintptr_t>(work) & 7) return hipErrorInvalidValue;
+  auto* key = static_cast<unsigned long long*>(work);
+  auto* cnt = reinterpret_cast<unsigned int*>(key + M);
   return by_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    hipLaunchKernelGGL(argmax_rows_kernel<T>, dim3(M), dim3(1024), 0, reinterpret_cast<hipStream_t>(stream),
-                       static_cast<const T*>(x), out, N);
+    const int vec = sizeof(T) == 2 && N % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const int parts = std::max(1, std::min(kArgMaxParts, (N + kArgSlice - 1) / kArgSlice));
+    hipLaunchKernelGGL(argmax_rows_kernel<T>, dim3(parts, M), dim3(kArgThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), static_cast<const T*>(x), out, N, vec, key, cnt);
+    return (int)hipGetLastError();
+  });
+}
+
+extern "C" int ssa_linear_swiglu(const void* x, const void* W, void* act, int32_t M, int32_t I, int32_t K,
+                                 int32_t dtype, void* stream) {
+  if (!x || !W || !act || M < 1 || M > 8 || I < 1 || K < 8 || K % 8) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) return hipErrorInvalidValue;
+  if (dtype != kBF16 && dtype != kF16) return hipErrorInvalidValue;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto go = [&](auto tag, auto mm) {
+    using T = decltype(tag);
+    constexpr int MM = decltype(mm)::value;
+    const int grid = (I + 7) / 8;
+    hipLaunchKernelGGL((swiglu_kernel<T, MM>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x),
+                       static_cast<const T*>(W), static_cast<T*>(act), M, I, K);
+    return (int)hipGetLastError();
+  };
+  auto bym = [&](auto tag) {
+    if (M <= 1) return go(tag, std::integral_constant<int, 1>{});
+    if (M <= 2) return go(tag, std::integral_constant<int, 2>{});
+    if (M <= 4) return go(tag, std::integral_constant<int, 4>{});
+    return go(tag, std::integral_constant<int, 8>{});
+  };
+  return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
+}
+
+extern "C" int ssa_embed_rmsnorm(const int64_t* tok, const void* embed, void* h, const void* w, void* x, int32_t rows,
+                                 int32_t D, int64_t vocab, float eps, const int64_t* pos, int32_t* n_out,
+                                 int32_t dtype, void* stream) {
+  if (!tok || !embed || !h || !w || !x || rows < 1 || D < 1 || vocab < 1 || (n_out && !pos)) return hipErrorInvalidValue;
+  return by_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL(embed_rmsnorm_kernel<T>, dim3(rows), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), tok,
+                       static_cast<const T*>(embed), static_cast<T*>(h), static_cast<const T*>(w), static_cast<T*>(x),
+                       D, vocab, eps, pos, n_out);
     return (int)hipGetLastError();
   });
 }

@@ -14,12 +14,16 @@ Insertion: with insert-ahead (``SphereIndexGraph.insert_ahead``, chosen per laye
 ``prepare``) each layer's step launch bins its next key; otherwise one ``AllLayerInsert`` launch
 bins every layer's key at the start of the step, as the reference's ``fused_insert`` does.
 
-Glue: with ``glue="fused"`` (the default) each layer is four projections (q/k/v, o, gate/up,
-down; the q/k/v and gate/up weights concatenated once; ``ssa_linear_skinny``, a weight-streaming
-kernel for the decode batch), the attention step, and three HIP kernels
-(``ssa_rmsnorm_add``: residual add + RMSNorm; ``ssa_qk_norm_rope_cache``: q/k RMSNorm, rotary
-embedding, KV-cache write; ``ssa_silu_mul``), instead of the ~60 element-wise launches of the
-model's own modules (``glue="torch"``, as the reference's ``_body`` runs them).
+Glue: with ``glue="fused"`` (the default) a layer is six launches besides the attention step:
+the q/k/v projection, ``ssa_qk_norm_rope_cache`` (q/k RMSNorm, rotary embedding, KV-cache write),
+the o projection, ``ssa_rmsnorm_add`` (residual add + RMSNorm), ``ssa_linear_swiglu`` (the
+gate/up projection with SwiGLU as its epilogue), the down projection and ``ssa_rmsnorm_add``; the
+projections are weight-streaming kernels for the decode batch (``ssa_linear_skinny``), the step
+opens with ``ssa_embed_rmsnorm`` and, with ``greedy``, ends with ``ssa_argmax_rows``.
+``glue="split"`` runs the gate/up projection and SwiGLU as two launches (the same bits), and
+``glue="torch"`` the ~60 element-wise launches of the model's own modules per layer, as the
+reference's ``_body`` runs them. At batch 1-2 every dependent launch costs a few microseconds
+whatever its size, so the launch count is what the glue is designed around.
 """
 
 from __future__ import annotations
@@ -79,15 +83,21 @@ class GraphDecoder:
         self._probe = None
         self.greedy = greedy
         self.next_tok = torch.zeros(B, 1, dtype=torch.long, device=dev)   # with greedy: argmax of the logits
+        self._argmax_work = torch.zeros(2 * B, dtype=torch.long, device=dev)  # ssa_argmax_rows' key + count
         self.fused_insert = fused_insert and mode == "cluster" and window >= 1
         self.insert_all = None
-        if glue not in ("fused", "torch"):
+        if glue not in ("fused", "split", "torch"):
             raise ValueError(f"unknown glue {glue!r}")
         self.glue = glue
-        if glue == "fused":
+        # "fused" folds SwiGLU into the gate/up projection where the kernel allows it (2-byte
+        # weights, batch <= 8); "split" runs the two ops as two launches (the same bits)
+        self._merge_gu = (glue == "fused" and dtype in (torch.bfloat16, torch.float16) and B <= 8
+                          and cfg.hidden_size % 8 == 0)
+        if glue != "torch":
             with torch.no_grad():
                 self._wqkv = [torch.cat((l.attn.q.weight, l.attn.k.weight, l.attn.v.weight)) for l in model.layers]
                 self._wgu = [torch.cat((l.ffn.gate.weight, l.ffn.up.weight)) for l in model.layers]
+            self._h = torch.empty(B, cfg.hidden_size, device=dev, dtype=dtype)     # the residual stream
             self._x = torch.empty(B, cfg.hidden_size, device=dev, dtype=dtype)
             self._qh = torch.empty(B * self.H, self.d, device=dev, dtype=dtype)
             self._act = torch.empty(B, cfg.intermediate_size, device=dev, dtype=dtype)
@@ -132,42 +142,45 @@ class GraphDecoder:
 
     def _body_fused(self) -> torch.Tensor:
         m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
-        L, s, x, eps, dt = len(m.layers), stream_ptr(self.tok.device), self._x, self._eps, self._dt
-        self.n_dev.copy_(self.pos + 1)
+        L, s, x, h, eps, dt = len(m.layers), stream_ptr(self.tok.device), self._x, self._h, self._eps, self._dt
+        act, I, D = self._act, self._act.shape[1], h.shape[1]
+        # h = embedding of the tokens, x = norm1(h), n_dev = pos + 1
+        check(lib().ssa_embed_rmsnorm(self.tok.data_ptr(), m.embed.weight.data_ptr(), h.data_ptr(),
+                                      m.layers[0].norm1.weight.data_ptr(), x.data_ptr(), B, D, m.embed.weight.shape[0],
+                                      eps, self.pos.data_ptr(), self.n_dev.data_ptr(), dt, s), "ssa_embed_rmsnorm")
         if self.insert_all is not None:
             self.insert_all(self.n_dev)
-        h = m.embed(self.tok).view(B, -1)                                  # the residual stream, updated in place
-        check(lib().ssa_rmsnorm_add(h.data_ptr(), None, m.layers[0].norm1.weight.data_ptr(), x.data_ptr(), B,
-                                    h.shape[1], eps, dt, s), "ssa_rmsnorm_add")
         for i, layer in enumerate(m.layers):
             a, f = layer.attn, layer.ffn
-            qkv = self._linear(x, self._wqkv[i])
             kc, vc = self.cache.k[i], self.cache.v[i]
-            check(lib().ssa_qk_norm_rope_cache(qkv.data_ptr(), a.q_norm.weight.data_ptr(), a.k_norm.weight.data_ptr(),
-                                               m.rope_cos.data_ptr(), m.rope_sin.data_ptr(), self.pos.data_ptr(),
-                                               self._qh.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0),
-                                               kc.stride(1), kc.stride(2), B, H, H_kv, d, eps, dt, s),
-                  "ssa_qk_norm_rope_cache")
+            rope = (a.q_norm.weight.data_ptr(), a.k_norm.weight.data_ptr(), m.rope_cos.data_ptr(),
+                    m.rope_sin.data_ptr(), self.pos.data_ptr(), self._qh.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                    kc.stride(0), kc.stride(1), kc.stride(2), B, H, H_kv, d)
+            qkv = self._linear(x, self._wqkv[i])
+            check(lib().ssa_qk_norm_rope_cache(qkv.data_ptr(), *rope, eps, dt, s), "ssa_qk_norm_rope_cache")
             out = self._attend(i, self._qh, kc, vc)
             o = self._linear(out.view(B, H * d), a.o.weight)
-            check(lib().ssa_rmsnorm_add(h.data_ptr(), o.data_ptr(), layer.norm2.weight.data_ptr(), x.data_ptr(), B,
-                                        h.shape[1], eps, dt, s), "ssa_rmsnorm_add")
-            gu = self._linear(x, self._wgu[i])
-            check(lib().ssa_silu_mul(gu.data_ptr(), self._act.data_ptr(), B, self._act.shape[1], dt, s),
-                  "ssa_silu_mul")
-            dn = self._linear(self._act, f.down.weight)
+            check(lib().ssa_rmsnorm_add(h.data_ptr(), o.data_ptr(), layer.norm2.weight.data_ptr(), x.data_ptr(), B, D,
+                                        eps, dt, s), "ssa_rmsnorm_add")
+            if self._merge_gu:
+                check(lib().ssa_linear_swiglu(x.data_ptr(), self._wgu[i].data_ptr(), act.data_ptr(), B, I, D, dt, s),
+                      "ssa_linear_swiglu")
+            else:
+                gu = self._linear(x, self._wgu[i])
+                check(lib().ssa_silu_mul(gu.data_ptr(), act.data_ptr(), B, I, dt, s), "ssa_silu_mul")
+            dn = self._linear(act, f.down.weight)
             nw = m.layers[i + 1].norm1.weight if i + 1 < L else m.final_norm.weight
-            check(lib().ssa_rmsnorm_add(h.data_ptr(), dn.data_ptr(), nw.data_ptr(), x.data_ptr(), B, h.shape[1], eps,
-                                        dt, s), "ssa_rmsnorm_add")
+            check(lib().ssa_rmsnorm_add(h.data_ptr(), dn.data_ptr(), nw.data_ptr(), x.data_ptr(), B, D, eps, dt, s),
+                  "ssa_rmsnorm_add")
         head = m.embed.weight if m.lm_head is None else m.lm_head.weight
         logits = self._linear(x, head)
         if self.greedy:
-            check(lib().ssa_argmax_rows(logits.data_ptr(), self.next_tok.data_ptr(), B, logits.shape[1], dt, s),
-                  "ssa_argmax_rows")
+            check(lib().ssa_argmax_rows(logits.data_ptr(), self.next_tok.data_ptr(), B, logits.shape[1], dt,
+                                        self._argmax_work.data_ptr(), s), "ssa_argmax_rows")
         return logits.view(B, 1, -1)
 
     def _body(self) -> torch.Tensor:
-        if self.glue == "fused":
+        if self.glue != "torch":
             return self._body_fused()
         m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
         self.n_dev.copy_(self.pos + 1)

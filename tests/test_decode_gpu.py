@@ -174,3 +174,89 @@ def test_greedy_token_is_the_argmax_of_the_logits():
             torch.cuda.synchronize()
             assert torch.equal(dec.next_tok, lg[:, -1].argmax(-1, keepdim=True)), pos
             tok = dec.next_tok.clone()
+
+
+CFG128 = Qwen3Config(vocab_size=96, hidden_size=256, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                     head_dim=128, intermediate_size=320, max_position_embeddings=512)
+
+
+@pytest.mark.parametrize("B", [1, 2, 3])
+def test_merged_glue_has_the_bits_of_the_split_glue(B):
+    """``glue="fused"`` (gate/up + SwiGLU in one launch) against ``glue="split"`` (two launches):
+    the same logits bit for bit, graph-captured, cluster mode."""
+    model = random_model(CFG128, dtype=torch.bfloat16, device="cuda", seed=5, std=0.2)
+    ids = torch.randint(0, CFG128.vocab_size, (B, P + T), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(5))
+    kw = dict(budget=0.2, C=16, window=4)
+    fused, dec = _graph_decode(model, ids, mode="cluster", capture=True, B=B, glue="fused", **kw)
+    split, _ = _graph_decode(model, ids, mode="cluster", capture=True, B=B, glue="split", **kw)
+    assert dec._merge_gu
+    assert torch.equal(fused, split)
+
+
+def _lib():
+    from ssa_amd._lib import check, dtype_tag, lib, stream_ptr
+    return check, dtype_tag, lib(), stream_ptr()
+
+
+@pytest.mark.parametrize("M,I,K", [(1, 3072, 1024), (2, 333, 264), (5, 100, 64), (8, 64, 2048)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_swiglu_projection_equals_skinny_then_silu_mul(M, I, K, dtype):
+    check, dtype_tag, L, s = _lib()
+    g = torch.Generator(device="cuda").manual_seed(M * 11 + I)
+    x = torch.randn(M, K, device="cuda", generator=g).to(dtype)
+    W = (torch.randn(2 * I, K, device="cuda", generator=g) * 0.05).to(dtype)
+    gu = torch.empty(M, 2 * I, device="cuda", dtype=dtype)
+    want = torch.empty(M, I, device="cuda", dtype=dtype)
+    got = torch.full((M, I), float("nan"), device="cuda", dtype=dtype)
+    check(L.ssa_linear_skinny(x.data_ptr(), W.data_ptr(), gu.data_ptr(), M, 2 * I, K, dtype_tag(dtype), s), "skinny")
+    check(L.ssa_silu_mul(gu.data_ptr(), want.data_ptr(), M, I, dtype_tag(dtype), s), "silu_mul")
+    check(L.ssa_linear_swiglu(x.data_ptr(), W.data_ptr(), got.data_ptr(), M, I, K, dtype_tag(dtype), s), "swiglu")
+    assert torch.equal(got, want)
+    ref = torch.nn.functional.silu(gu[:, :I].float()).to(dtype).float() * gu[:, I:].float()
+    torch.testing.assert_close(got.float(), ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_embed_rmsnorm_equals_embedding_then_rmsnorm(dtype):
+    check, dtype_tag, L, s = _lib()
+    g = torch.Generator(device="cuda").manual_seed(9)
+    V, D, B = 500, 1024, 3
+    emb = torch.randn(V, D, device="cuda", generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).to(dtype)
+    tok = torch.tensor([[7], [499], [0]], device="cuda", dtype=torch.long)
+    pos = torch.tensor([41], device="cuda", dtype=torch.long)
+    n = torch.zeros(1, device="cuda", dtype=torch.int32)
+    h, x = torch.empty(B, D, device="cuda", dtype=dtype), torch.empty(B, D, device="cuda", dtype=dtype)
+    check(L.ssa_embed_rmsnorm(tok.data_ptr(), emb.data_ptr(), h.data_ptr(), w.data_ptr(), x.data_ptr(), B, D, V, 1e-6,
+                              pos.data_ptr(), n.data_ptr(), dtype_tag(dtype), s), "embed_rmsnorm")
+    h2 = emb[tok.view(-1)].clone()
+    x2 = torch.empty_like(x)
+    check(L.ssa_rmsnorm_add(h2.data_ptr(), None, w.data_ptr(), x2.data_ptr(), B, D, 1e-6, dtype_tag(dtype), s),
+          "rmsnorm_add")
+    assert torch.equal(h, h2) and torch.equal(x, x2) and int(n) == 42
+
+
+@pytest.mark.parametrize("N", [151936, 1001, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_argmax_rows_is_torch_argmax(N, dtype):
+    """First index of the maximum, with planted ties (the earlier copy wins) and a NaN row."""
+    check, dtype_tag, L, s = _lib()
+    g = torch.Generator(device="cuda").manual_seed(N)
+    x = torch.randn(4, N, device="cuda", generator=g).to(dtype)
+    x[1, N // 3] = 50.0
+    x[1, N - 1] = 50.0                                  # a tie: the first copy wins
+    x[2] = 1.0                                          # all equal: index 0
+    x[3, N // 2] = float("nan")
+    x[3, N // 4] = 60.0
+    x[0, 5] = -0.0 if N > 8 else x[0, 5]
+    work = torch.zeros(8, device="cuda", dtype=torch.long)
+    for _ in range(2):                                  # the work buffer is left zero for the next call
+        out = torch.full((4,), -1, device="cuda", dtype=torch.long)
+        check(L.ssa_argmax_rows(x.data_ptr(), out.data_ptr(), 4, N, dtype_tag(dtype), work.data_ptr(), s), "argmax")
+        assert torch.equal(out, x.argmax(-1)), (out, x.argmax(-1))
+        assert not work.any()
+    z = torch.zeros(1, N, device="cuda", dtype=dtype)
+    z[0, 3] = -0.0                                      # -0 and +0 are equal: the first index wins
+    check(L.ssa_argmax_rows(z.data_ptr(), out.data_ptr(), 1, N, dtype_tag(dtype), work.data_ptr(), s), "argmax")
+    assert int(out[0]) == 0
