@@ -409,8 +409,15 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
       continue;
     }
     float nrm2_i[8], dot_i[8][GMAX];
+    const int kact = min(C, n_act);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      if (256 * k + 32 * i >= kact) {            // rows [256k + 32i, +32) hold no slot in use (uniform)
+        nrm2_i[i] = 0.f;
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) dot_i[i][g] = 0.f;
+        continue;
+      }
       const int cr = min(grp + 256 * k + 32 * i, C - 1);        // rows past C are never kept
       float x[E];
       if (H.q8dirs) {
