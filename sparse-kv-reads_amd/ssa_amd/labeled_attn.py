@@ -39,11 +39,15 @@ def default_splits(device, n_heads: int, *, dense: bool = False) -> int:
     kernel takes two workgroups per compute unit: each reads a scattered row list, and one
     resident workgroup per compute unit leaves bandwidth unused (measured on MI355X at 32k
     context: batch 16 goes from 157 to 128 us at 20%, while smaller batches lose to the longer
-    merge)."""
+    merge). With few heads (16 splits or more) the sparse kernel takes 1.5 workgroups per compute
+    unit, so that the row phase of one overlaps the selection phase of another (batch 2 x 32k at
+    20%: 48.6 us at 16 splits, 45.0 us at 24, 57.1 us at 32; one head per 32 splits is the cap)."""
     cus = cu_count(device)
     s = -(-cus // n_heads)
     if not dense and s <= 2:
         s = -(-2 * cus // n_heads)
+    elif not dense and s >= 16:
+        s = -(-3 * cus // (2 * n_heads))
     return max(1, min(32, s))
 
 
