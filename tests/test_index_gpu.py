@@ -247,3 +247,40 @@ def test_fused_step_shapes_match_the_oracle(H, H_kv, d, dtype, group):
                                         V.double().cpu().numpy(), canon.labels[:, :n], want_w)
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=tol)
+
+
+@pytest.mark.parametrize("budget", [0.2, 0.05])
+def test_config1_full_size_selection_and_output(budget):
+    """configs[1] at its full size (B=1, 16 q / 8 kv heads, d=128, bf16, n=32768, 256 k-means
+    clusters, window 64) through the fused step. The 10-iteration fit at 32k is too slow for the
+    C oracle in a test, so the oracle takes the GPU's fitted state (``CanonIndex.from_gpu``) and
+    restates what the north_star contract pins given identical summaries: the selection ``w`` and
+    the selected positions, bit for bit; the summaries against a recount of the labels; the
+    output against the float64 spec (2e-2)."""
+    from ssa_amd.labeled_attn import compact_positions
+    n, C, W = 32768, 256, 64
+    K, V, q = _keys(8, n + 64, H=16, seed=3, dtype=torch.bfloat16, centers=256)
+    idx = _fused(C=C, window=W, delta=0.03, capacity=n + 64, check_every=10 ** 9)
+    out, labels, w = idx.attend(q, K, V, n=n, budget=budget)
+    torch.cuda.synchronize()
+    canon = CanonIndex.from_gpu(idx)
+    end = n - W
+    lab = canon.labels[:, :n].astype(np.int64)
+    assert (lab[:, 0] == C).all() and (lab[:, end:] == C).all()          # sink and window: exact set
+    assert (lab[:, 1:end] < canon.n_c[:, None]).all()
+    for h in range(8):
+        assert np.array_equal(np.bincount(lab[h, 1:end], minlength=C)[:C], canon.count[h].astype(np.int64))
+    want_w = canon.select(q, budget=budget)
+    got_w = w.cpu().numpy()
+    assert np.array_equal(got_w, want_w)
+    need = math.ceil(budget * (end - 1))
+    for h in range(8):
+        sel = got_w[h, :C] > 0
+        assert got_w[h, C] == 1.0 and int(canon.count[h][sel].sum()) >= need
+    idx_list, cnt = compact_positions(labels, w)
+    want_idx = canon.compact(want_w, n)
+    for h in range(8):
+        assert np.array_equal(idx_list[h, :int(cnt[h])].cpu().numpy(), want_idx[h])
+    want = ref.label_weighted_attention(q.double().cpu().numpy(), K[:, :n].double().cpu().numpy(),
+                                        V[:, :n].double().cpu().numpy(), lab, want_w)
+    np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=2e-2)
