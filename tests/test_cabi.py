@@ -1,6 +1,6 @@
 """The C ABI (CPU only): libssa_hip.so loads, exports every function include/ssa_hip.h declares,
 and the ctypes mirrors of the header's structs have the C layout (checked against gcc's).
-No entry point is called: there is no GPU here."""
+No entry point launches anything: there is no GPU here (argument checks return first)."""
 
 from __future__ import annotations
 
@@ -68,3 +68,19 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.lib()
+
+
+def test_glue_entry_points_refuse_bad_arguments_before_any_launch():
+    """Null pointers, empty or oversized batches and a missing work buffer are refused on the host
+    (a nonzero return before any HIP call), so nothing here needs a GPU."""
+    h = _lib_handle()
+    fake = 1 << 20                                       # never dereferenced: every call returns early
+    assert h.ssa_linear_swiglu(None, fake, fake, 2, 64, 64, 1, None) != 0
+    assert h.ssa_linear_swiglu(fake, fake, fake, 9, 64, 64, 1, None) != 0      # batch above 8
+    assert h.ssa_linear_swiglu(fake, fake, fake, 2, 64, 60, 1, None) != 0      # K not a multiple of 8
+    assert h.ssa_linear_swiglu(fake, fake, fake, 2, 64, 64, 0, None) != 0      # fp32 weights
+    assert h.ssa_linear_skinny(fake, fake, fake, 0, 64, 64, 1, None) != 0
+    assert h.ssa_argmax_rows(fake, fake, 2, 100, 1, None, None) != 0           # no work buffer
+    assert h.ssa_argmax_rows(fake, fake, 0, 100, 1, fake, None) != 0
+    assert h.ssa_embed_rmsnorm(None, fake, fake, fake, fake, 2, 64, 10, 1e-6, fake, fake, 1, None) != 0
+    assert h.ssa_embed_rmsnorm(fake, fake, fake, fake, fake, 2, 64, 10, 1e-6, None, fake, 1, None) != 0
