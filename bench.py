@@ -379,9 +379,8 @@ def batched_sweep(args, dev) -> dict:
         advance = lambda: n_all.add_(1)                               # noqa: E731
         gd = capture([lambda s=s: s[4](s[2], s[0], s[1], s[5]) for s in sets])
         time_graph(gd, 3, rot)
-        dense_us = time_graph(gd, reps, rot)[0]
-        row = {"rotation_caches": rot, "kv_heads": hk, "splits": sets[0][3].work.S, "dense_us": round(dense_us, 2),
-               "dense_GBs": round(kv_bytes / dense_us / 1e3, 1)}
+        dense_first = time_graph(gd, reps, rot)[0]
+        row = {"rotation_caches": rot, "kv_heads": hk, "splits": sets[0][3].work.S}
         for b in BATCHED_BUDGETS:
             for s in sets:
                 s[3].budget = b
@@ -408,9 +407,17 @@ def batched_sweep(args, dev) -> dict:
                 "step_us_insert_ahead": round(ahead[True], 2), "step_us_insert_launch": round(ahead[False], 2),
                 "rows_per_head": int(sum(rows) / len(rows)),
                 "attention_GBs": round(by / attn_us / 1e3, 1), "attention_frac": round(by / attn_us / 1e3 / PEAK_GBS, 4),
-                "step_effective_GBs": round(step_bytes(rows, n) / step_us / 1e3, 1),
-                "speedup_vs_dense": round(dense_us / step_us, 2)}
+                "step_effective_GBs": round(step_bytes(rows, n) / step_us / 1e3, 1)}
             del ga
+        # dense is timed again after the sparse runs, at the same length, and the faster time is
+        # the baseline: the first timing, right after the caches' prefill, can run slow
+        n_all.fill_(n)
+        time_graph(gd, 3, rot)
+        dense_us = min(dense_first, time_graph(gd, reps, rot)[0])
+        row.update({"dense_us": round(dense_us, 2), "dense_us_first": round(dense_first, 2),
+                    "dense_GBs": round(kv_bytes / dense_us / 1e3, 1)})
+        for b in BATCHED_BUDGETS:
+            row[f"{int(b * 100)}%"]["speedup_vs_dense"] = round(dense_us / row[f"{int(b * 100)}%"]["step_us"], 2)
         out[f"{B}x{n}"] = row
         log(json.dumps({f"{B}x{n}": row}))
         del sets, gd
