@@ -113,6 +113,14 @@ constexpr int kMergeBatch = 8;       // accumulator loads (float4) each merging 
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Four consecutive floats (16-byte aligned) as two 8-byte agent-scope relaxed loads.
+__device__ __forceinline__ float4 load_coherent4(const float* p) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((unsigned int)a), __uint_as_float((unsigned int)(a >> 32)),
+                     __uint_as_float((unsigned int)b), __uint_as_float((unsigned int)(b >> 32)));
+}
 
 template <int D, int GMAX, bool DENSE>
 struct DecodeSmem {
@@ -458,48 +466,48 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   __syncthreads();
   if (!sm.last) return;
   // ---- the last workgroup of head h merges the S partials ----------------------------------
-  // One round of loads, all issued before the first wait: this thread's accumulator columns
-  // (up to kMergeBatch splits) into registers and, in wave 0, every split's (max, sum) and row
-  // count spread over the lanes. The partials are read with agent-scope loads (coherent across
-  // XCDs), so no L2 invalidate is needed.
+  // One round of loads, all issued before the first wait: in wave 0, every split's (max, sum)
+  // and row count spread over the lanes, first, so that the rescale factors can be computed
+  // while the rest arrives; then this thread's accumulator columns (up to kMergeBatch splits)
+  // into registers. The partials are read with agent-scope loads (coherent across XCDs), so no
+  // L2 invalidate is needed.
   const int64_t hb = (int64_t)h * S;
   const int cols4 = G * D / 4;
   const float* pa = a.part_a + hb * G * D;
   const int ncol0 = min(kThreads, cols4);
   const int nsg0 = kThreads / ncol0;
   const int sg0 = tid / ncol0, col0 = tid % ncol0;
-  // branchless: out-of-range splits re-read split S-1 and get weight 0 below
-  float4 va[kMergeBatch];
-#pragma unroll
-  for (int k = 0; k < kMergeBatch; ++k) {
-    const int s2 = min(sg0 + k * nsg0, S - 1);
-    const float* src = pa + ((int64_t)s2 * cols4 + col0) * 4;
-    va[k].x = load_coherent(src + 0);
-    va[k].y = load_coherent(src + 1);
-    va[k].z = load_coherent(src + 2);
-    va[k].w = load_coherent(src + 3);
-  }
+  // wave 0: lane l holds head g = l % GMAX of splits l / GMAX + (64 / GMAX) * i
+  constexpr int SPI = 64 / GMAX;                        // splits per round of lanes
+  constexpr int kML = (kMaxS + SPI - 1) / SPI;
+  const int gl = lane % GMAX;
+  float mv[kML], lv[kML];
+  int cpart = 0;
   if (wave == 0) {
-    // lane l holds head g = l % GMAX of splits l / GMAX + (64 / GMAX) * i
-    constexpr int SPI = 64 / GMAX;                      // splits per round of lanes
-    constexpr int kML = (kMaxS + SPI - 1) / SPI;
-    const int g = lane % GMAX;
-    float mv[kML], lv[kML];
-    int cpart = 0;
 #pragma unroll
     for (int i = 0; i < kML; ++i) {
       if (i * SPI < S) {                                // uniform
         const int s2 = lane / GMAX + SPI * i;
-        const int e = min(s2, S - 1) * G + min(g, G - 1);
+        const int e = min(s2, S - 1) * G + min(gl, G - 1);
         const float m0 = load_coherent(a.part_m + hb * G + e);
         const float l0 = load_coherent(a.part_l + hb * G + e);
-        const bool ok = s2 < S && g < G;
+        const bool ok = s2 < S && gl < G;
         mv[i] = ok ? m0 : kNeg;
         lv[i] = ok ? l0 : 0.f;
       }
     }
     for (int t = lane; t < S; t += 64)
       cpart += __hip_atomic_load(a.part_cnt + hb + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // branchless: out-of-range splits re-read split S-1 and get weight 0 below
+  float4 va[kMergeBatch];
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) {
+    const int s2 = min(sg0 + k * nsg0, S - 1);
+    va[k] = load_coherent4(pa + ((int64_t)s2 * cols4 + col0) * 4);
+  }
+  if (wave == 0) {
+    const int g = gl;
     float M = kNeg;
 #pragma unroll
     for (int i = 0; i < kML; ++i)
@@ -545,9 +553,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
 #pragma unroll 8
       for (; s2 < S; s2 += nsg) {
         const float f = sm.u.mrg.f[s2 * G + g];
-        const float* src = pa + ((int64_t)s2 * cols4 + col) * 4;
-        acc4.x = fmaf(f, load_coherent(src + 0), acc4.x); acc4.y = fmaf(f, load_coherent(src + 1), acc4.y);
-        acc4.z = fmaf(f, load_coherent(src + 2), acc4.z); acc4.w = fmaf(f, load_coherent(src + 3), acc4.w);
+        const float4 v4 = load_coherent4(pa + ((int64_t)s2 * cols4 + col) * 4);
+        acc4.x = fmaf(f, v4.x, acc4.x); acc4.y = fmaf(f, v4.y, acc4.y);
+        acc4.z = fmaf(f, v4.z, acc4.z); acc4.w = fmaf(f, v4.w, acc4.w);
       }
     }
     if (c0 > 0) __syncthreads();     // the previous chunk's sums have been read
