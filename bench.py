@@ -409,8 +409,8 @@ def batched_sweep(args, dev) -> dict:
                 "attention_GBs": round(by / attn_us / 1e3, 1), "attention_frac": round(by / attn_us / 1e3 / PEAK_GBS, 4),
                 "step_effective_GBs": round(step_bytes(rows, n) / step_us / 1e3, 1)}
             del ga
-        # dense is timed again after the sparse runs, at the same length, and the faster time is
-        # the baseline: the first timing, right after the caches' prefill, can run slow
+        # dense is timed again after the sparse runs, at the same length, and the faster of the two
+        # timings is the baseline
         n_all.fill_(n)
         time_graph(gd, 3, rot)
         dense_us = min(dense_first, time_graph(gd, reps, rot)[0])
