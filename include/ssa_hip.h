@@ -137,7 +137,8 @@ int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const 
 /* One layer's decode step after insertion, in one launch: every workgroup of the attention grid
  * computes its head's selection exactly as ssa_select does (same bits, from the index state and
  * sel), then attends over the selected rows as ssa_label_attention does. args->labels must be
- * st->labels; sel->w, if non-NULL, receives the selection (written by one workgroup per head).
+ * st->labels with args->s_lh = st->capacity (refused otherwise); sel->w, if non-NULL, receives
+ * the selection (written by one workgroup per head).
  * With ins_ahead non-NULL (one layer's state, ins_ahead->k the attention's K, no koff), once
  * every workgroup of a head has read the state, the last one inserts the keys that leave the
  * window at length n + 1 (ins_ahead's n fields are ignored), splits included: the state is then

@@ -124,6 +124,8 @@ int launch_decode(const ssa_attn_args_t* x, int mode, void* stream, const ssa_in
     if (!st || !sel || st->C < 16 || st->C > kMaxC || (st->C & (st->C - 1)) || st->d != x->d || sel->G != x->G ||
         st->n_heads != x->n_heads || sel->group < 0 || sel->group > 3)
       return hipErrorInvalidValue;
+    // the selection is computed from the state, so the labels scanned must be the state's own rows
+    if (x->labels != st->labels || x->s_lh != st->capacity || st->capacity < 1) return hipErrorInvalidValue;
     p.st = *st;
     p.budget = sel->budget;
     p.group = sel->group;

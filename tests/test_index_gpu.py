@@ -284,3 +284,24 @@ def test_config1_full_size_selection_and_output(budget):
     want = ref.label_weighted_attention(q.double().cpu().numpy(), K[:, :n].double().cpu().numpy(),
                                         V[:, :n].double().cpu().numpy(), lab, want_w)
     np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=2e-2)
+
+
+def test_fused_step_refuses_labels_other_than_the_state_rows():
+    """ssa_sparse_step computes its selection from the index state, so it accepts only the
+    state's own label buffer with its row stride (hipErrorInvalidValue = 1 otherwise)."""
+    from ssa_amd._lib import lib, stream_ptr
+    from ssa_amd.labeled_attn import SplitWork, attn_args
+    K, V, q = _keys(4, 600, H=8, seed=2, dtype=torch.bfloat16, centers=16)
+    idx = _fused(C=16, window=16, capacity=600)
+    idx.attend(q, K, V, n=600, budget=0.2)
+    w = idx._wbuf("sum_share", 4)
+    work = SplitWork(4, 2, 2, 128, q.device)
+    out = torch.empty_like(q)
+    st, sel = idx._state(), idx._select_args(q, w, 0.2, "sum_share")
+    wider = torch.full((4, idx.capacity + 64), 0, device="cuda", dtype=idx.labels.dtype)
+    for labels in (idx.labels.clone(), wider):
+        a = attn_args(q, K, V, out, work, labels=labels, w=w, n_host=600)
+        assert lib().ssa_sparse_step(st, sel, a, None, stream_ptr(q.device)) == 1
+    a = attn_args(q, K, V, out, work, labels=idx.labels, w=w, n_host=600)
+    assert lib().ssa_sparse_step(st, sel, a, None, stream_ptr(q.device)) == 0
+    torch.cuda.synchronize()
