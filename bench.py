@@ -131,64 +131,90 @@ def time_graph(g, reps, per, *, advance=None):
 
 
 def cpu_baseline(seconds: float):
-    """The oracle's numpy restatement of the reference CPU path at the config-1 shape (fp32):
-    per step one key observed, labels_and_weights, label_weighted_attention."""
+    """The reference's CPU path, restated in PyTorch (oracle/torch_ref.py), on this host's cores at
+    the configs[1] shape in fp32 (the reference computes in fp32, src/ssa/attn/geometry.py:20-24):
+    per step one key observed, labels_and_weights (sum_share) and label_weighted_attention over
+    every cached key, as src/ssa/attn/labeled.py:24-44 computes it. Beside it, the oracle's numpy
+    port that reads only the selected rows (the same selection, the attention restricted to the
+    rows the GPU reads), and the configs[0] case (n = 4096) of the reference-shaped path."""
     import numpy as np
     import torch
     from oracle.reference import SphereIndexRef
+    from oracle.torch_ref import SphereIndexTorch
     from ssa_amd.sphere_fused import kmeans_init_indices
     from ssa_amd.synth import make_cache
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:
-        threads = 1
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     K, V, q, _ = make_cache(1, H_KV, N + 64, D, H=H, centers=C, seed=0, dtype=torch.float32)
-    K, V, q = K[0].numpy(), V[0].numpy(), q[0].numpy()
-    ref = SphereIndexRef(C=C, window=WINDOW, init_indices=lambda m, c, s: kmeans_init_indices(m, c, s).numpy())
+    K, V, q = K[0].contiguous(), V[0].contiguous(), q[0].contiguous()
+    init = lambda m, c: kmeans_init_indices(m, c, 0)                      # noqa: E731
+    ref = SphereIndexTorch(C=C, window=WINDOW, init_indices=init)
     t0 = time.time()
     ref.observe(K, N)
     prefill = time.time() - t0
     times, rows = [], []
     n = N
-    t_end = time.time() + seconds
-    while time.time() < t_end and n < N + 64:
-        n += 1
-        t = time.time()
-        out, labels, w = ref.attend(q, K, V, n=n, budget=HEADLINE, fast=True)
-        times.append(time.time() - t)
-        rows = [int((w[h][labels[h].astype(np.int64)] > 0).sum()) for h in range(H_KV)]
+    t_end = time.time() + seconds * 0.6
+    with torch.inference_mode():
+        while time.time() < t_end and n < N + 64:
+            n += 1
+            t = time.time()
+            _, labels, w = ref.attend(q, K, V, n=n, budget=HEADLINE)
+            times.append(time.time() - t)
+            rows = [int((w[h][labels[h].long()] > 0).sum()) for h in range(H_KV)]
     times.sort()
     med = times[len(times) // 2]
-    # configs[0] exactly: n = 4096, the same path, 20 steps
+    # the numpy port reading only the selected rows, same shape and steps
+    port = SphereIndexRef(C=C, window=WINDOW, init_indices=lambda m, c, s: kmeans_init_indices(m, c, s).numpy())
+    Kn, Vn, qn = K.numpy(), V.numpy(), q.numpy()
+    port.observe(Kn, N)
+    pt, m = [], N
+    t_end = time.time() + seconds * 0.25
+    while time.time() < t_end and m < N + 64:
+        m += 1
+        t = time.time()
+        port.attend(qn, Kn, Vn, n=m, budget=HEADLINE, fast=True)
+        pt.append(time.time() - t)
+    pt.sort()
+    # configs[0] exactly: n = 4096, the reference-shaped path, 20 steps
     n0 = 4096
     K0, V0, q0, _ = make_cache(1, H_KV, n0 + 32, D, H=H, centers=C, seed=0, dtype=torch.float32)
-    K0, V0, q0 = K0[0].numpy(), V0[0].numpy(), q0[0].numpy()
-    ref0 = SphereIndexRef(C=C, window=WINDOW, init_indices=lambda m, c, s: kmeans_init_indices(m, c, s).numpy())
+    K0, V0, q0 = K0[0].contiguous(), V0[0].contiguous(), q0[0].contiguous()
+    ref0 = SphereIndexTorch(C=C, window=WINDOW, init_indices=init)
     ref0.observe(K0, n0)
     t0s = []
-    for k in range(1, 21):
-        t = time.time()
-        ref0.attend(q0, K0, V0, n=n0 + k, budget=HEADLINE, fast=True)
-        t0s.append(time.time() - t)
+    with torch.inference_mode():
+        for k in range(1, 21):
+            t = time.time()
+            ref0.attend(q0, K0, V0, n=n0 + k, budget=HEADLINE)
+            t0s.append(time.time() - t)
     t0s.sort()
-    return {"value": step_bytes(rows, n) / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_step": med * 1e6, "prefill_s": prefill,
-            "config0_us_per_step": t0s[len(t0s) // 2] * 1e6,
-            "sample": f"{len(times)} decode steps at n={N}..{n}, fp32, B=1, 16/8 heads, d=128, C=256, "
-                      f"budget {HEADLINE}, after one k-means prefill ({prefill:.1f} s); median step "
-                      f"(config0_us_per_step: the same path at configs[0], n=4096, median of 20 steps)",
+    return {"value": round(step_bytes(rows, n) / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "us_per_step": round(med * 1e6, 1), "prefill_s": round(prefill, 2),
+            "sparse_port_us_per_step": round(pt[len(pt) // 2] * 1e6, 1) if pt else None,
+            "config0_us_per_step": round(t0s[len(t0s) // 2] * 1e6, 1),
+            "sample": f"{len(times)} decode steps at n={N}..{n}, fp32, B=1, 16/8 heads, d=128, C=256, budget "
+                      f"{HEADLINE}, after one k-means prefill ({prefill:.1f} s); median step of the reference-shaped "
+                      f"PyTorch path (all {N} keys scored, then masked); sparse_port_us_per_step: the numpy port "
+                      f"that reads only the selected rows ({len(pt)} steps); config0_us_per_step: the "
+                      f"reference-shaped path at configs[0], n=4096, median of 20 steps",
+            "threads": torch.get_num_threads(), "cpu_count": os.cpu_count(), "affinity": cores,
             "cpu": _cpu_model()}
 
 
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (model name, family / model / stepping)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info.setdefault(k.strip(), v.strip())
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    return f"{name} (family {info.get('cpu family', '?')}, model {info.get('model', '?')}, " \
+           f"stepping {info.get('stepping', '?')})"
 
 
 def main() -> int:
@@ -235,18 +261,19 @@ def main() -> int:
         return 0
     if args.config == 2:
         res = batched_sweep(args, dev)
-        print(json.dumps({"metric": "configs[2] batched sparse decode-attention sweep (us, GB/s)", "unit": "us",
-                          "n_gpus": 1, "dtype": "bf16", "data": "synthetic (ssa_amd.synth)", "peak_GBs": PEAK_GBS,
-                          "config": {"workload": "configs[2]: B x ctx in " + str(list(BATCHED)) + ", 16 q / 8 kv "
-                                     "heads per sequence, d=128, bf16, 256 k-means clusters, window 64",
-                                     "budgets": list(BATCHED_BUDGETS)},
-                          "results": res}), flush=True)
+        print(json.dumps(_stamped({"metric": "configs[2] batched sparse decode-attention sweep (us, GB/s)",
+                                   "unit": "us", "n_gpus": 1, "dtype": "bf16", "data": "synthetic (ssa_amd.synth)",
+                                   "peak_GBs": PEAK_GBS,
+                                   "config": {"workload": "configs[2]: B x ctx in " + str(list(BATCHED)) + ", 16 q / "
+                                              "8 kv heads per sequence, d=128, bf16, 256 k-means clusters, window 64",
+                                              "budgets": list(BATCHED_BUDGETS)},
+                                   "results": res})), flush=True)
         return 0
     if args.config == 3:
-        print(json.dumps(model_decode(args, dev)), flush=True)
+        print(json.dumps(_stamped(model_decode(args, dev))), flush=True)
         return 0
     if args.config == 4:
-        print(json.dumps(model_long(args, dev)), flush=True)
+        print(json.dumps(_stamped(model_long(args, dev))), flush=True)
         return 0
     global BUDGETS
     if args.budgets:
@@ -255,7 +282,7 @@ def main() -> int:
             BUDGETS = BUDGETS + (HEADLINE,)
     splits = args.splits or None
     reps = max(args.steps // args.rot, 4)
-    extra = (args.warmup + 3) * len(BUDGETS) + reps * (len(BUDGETS) + 1) + 64
+    extra = (args.warmup + 3) * len(BUDGETS) + reps * (len(BUDGETS) + 1) + 3 * (args.steps // args.rot + 2) + 64
     n_all = torch.full((args.rot,), N, dtype=torch.int32, device=dev)
     log(f"building {args.rot} caches of {N} tokens ...")
     sets = [Set(s, N, extra, splits, dev, n_all[s:s + 1], args.dense_splits or None) for s in range(args.rot)]
@@ -282,17 +309,28 @@ def main() -> int:
     time_graph(graphs["dense"], 3, R)
     res["dense"] = time_graph(graphs["dense"], reps, R)
 
-    # the timed region: exactly K steps at the headline budget (K/rot replays of the rot-step
-    # graph), bracketed by synchronisations
-    g = graphs[("step", HEADLINE)]
+    # The timed region: exactly K steps at the headline budget, as one graph that walks the
+    # caches in turn and advances every length after each full round of them, bracketed by
+    # synchronisations.
+    for st in sets:
+        st.idx.budget = HEADLINE
+    K_steps = max(1, args.steps)
+    seq = []
+    for k in range(K_steps):
+        st = sets[k % R]
+        seq.append(lambda st=st: st.idx.step(st.q, st.K, st.V, st.n_dev))
+        if k % R == R - 1 and k + 1 < K_steps:
+            seq.append(advance)
+    advance()
+    g = capture(seq)
+    g.replay()                                                        # untimed: graph upload
+    advance()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
-        advance()
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    steps_timed = reps * R
+    steps_timed = K_steps
     n_now = int(n_all[0])
 
     dense_us = res["dense"][0]
@@ -335,8 +373,15 @@ def main() -> int:
     if not args.no_cpu:
         log("timing the CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-    print(json.dumps(out), flush=True)
+    print(json.dumps(_stamped(out)), flush=True)
     return 0
+
+
+def _stamped(line: dict) -> dict:
+    """The JSON line with the provenance header appended (src/ssa/harness/stamp.py:35-45): the
+    driver's fields stay first, the header goes under "provenance"."""
+    from ssa_amd.stamp import stamp
+    return {**line, "provenance": stamp({})}
 
 
 BATCHED = ((8, 8192), (2, 32768), (16, 32768), (64, 32768))

@@ -35,7 +35,7 @@ typedef struct ssa_attn_args {
   const float* w; int64_t s_wr; int32_t w_len; int32_t per_head;
   const int32_t* n_dev; int32_t n_host;      /* positions [0, n) are attended; n_dev wins if set */
   float* part_m; float* part_l;              /* [Hk, S, G] split partials (base-2 log domain) */
-  float* part_a;                             /* [Hk, S, G, d] */
+  float* part_a;                             /* [Hk, S, G, d], 16-byte aligned */
   int32_t* part_cnt;                         /* [Hk, S] rows read per split */
   int32_t* counter;                          /* [Hk] zero on first use; the kernel leaves it zero */
   void* out; int64_t s_oh; int32_t out_dtype;/* [Hk*G, d] */
@@ -44,6 +44,10 @@ typedef struct ssa_attn_args {
   int32_t chunk_align;                       /* dense: split boundaries are multiples of it; label
                                                 scans: split s reads blocks of 256 positions b = s mod S */
 } ssa_attn_args_t;
+/* q, k, v and part_a must be 16-byte aligned and every row stride (s_qh, s_kh, s_kn, s_vh, s_vn
+ * times the element size, and d times the element size) a multiple of 16 bytes: rows are read
+ * as 16-byte vectors. The attention entry points return hipErrorInvalidValue otherwise, before
+ * anything is launched. */
 
 /* Label-weighted split-K decode attention with the compaction fused in: positions whose label
  * has positive weight (for any query head of the group when per_head) are read, each with

@@ -134,50 +134,41 @@ static void ordered_sums(const float* K, int d, const float* mu, const int* mem,
   free(kn); free(b0); free(b1);
 }
 
-static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {
-  const int d = H->d;
-  int* mem = (int*)malloc(sizeof(int) * (size_t)(stop > 0 ? stop : 1));
-  int m = 0;
-  for (int j = 1; j < stop; ++j)
-    if (H->labels[j] == c && m < H->ms) mem[m++] = j;
-  if (m < 2) { free(mem); return; }
-  float* mag = (float*)malloc(sizeof(float) * m);
-  float* proj = (float*)malloc(sizeof(float) * m);
-  int* side = (int*)malloc(sizeof(int) * m);
-  float* kr = (float*)malloc(sizeof(float) * d);
+/* The bisection of _bisect_padded (src/ssa/attn/sphere_gpu.py:76-102) on the members mem[0..m)
+ * (key rows of K, centred by mu, lengths mag): 2-means from the first member and the member least
+ * similar to it, 4 updates, then the final sides; a result with fewer than 25% or more than 75% of
+ * the members on side 1 is replaced by the cut at the median projection on b - a (stable order). */
+void canon_bisect(const float* K, int d, const float* mu, const int* mem, const float* mag, int m, int* side) {
+  float* proj = (float*)malloc(sizeof(float) * (size_t)(m > 0 ? m : 1));
   float* kn = (float*)malloc(sizeof(float) * d);
   float* a = (float*)malloc(sizeof(float) * d);
   float* b = (float*)malloc(sizeof(float) * d);
   float* s0 = (float*)malloc(sizeof(float) * d);
   float* s1 = (float*)malloc(sizeof(float) * d);
   float* vs = (float*)malloc(sizeof(float) * d);
-  for (int j = 0; j < m; ++j) {
-    for (int i = 0; i < d; ++i) kr[i] = K[(int64_t)mem[j] * d + i] - H->mu_ref[i];
-    mag[j] = sqrtf(canon_dot(kr, kr, d));
-  }
-  kn_of(K, d, H->mu_ref, mem[0], fmaxf(mag[0], 1e-12f), a);
+  kn_of(K, d, mu, mem[0], fmaxf(mag[0], 1e-12f), a);
   float lo = 0.f;
   int far = -1;
   for (int j = 0; j < m; ++j) {
-    kn_of(K, d, H->mu_ref, mem[j], fmaxf(mag[j], 1e-12f), kn);
+    kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
     float sim = canon_dot(kn, a, d);
     if (far < 0 || sim < lo) { lo = sim; far = j; }
   }
-  kn_of(K, d, H->mu_ref, mem[far], fmaxf(mag[far], 1e-12f), b);
+  kn_of(K, d, mu, mem[far], fmaxf(mag[far], 1e-12f), b);
   int n1 = 0;
   for (int it = 0; it < 4; ++it) {
     for (int j = 0; j < m; ++j) {
-      kn_of(K, d, H->mu_ref, mem[j], fmaxf(mag[j], 1e-12f), kn);
+      kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
       side[j] = canon_dot(kn, b, d) > canon_dot(kn, a, d);
     }
-    ordered_sums(K, d, H->mu_ref, mem, mag, side, m, s0, s1, &n1);
+    ordered_sums(K, d, mu, mem, mag, side, m, s0, s1, &n1);
     if (m - n1 > 0) unit(s0, a, d);
     if (n1 > 0) unit(s1, b, d);
   }
   for (int i = 0; i < d; ++i) vs[i] = b[i] - a[i];
   n1 = 0;
   for (int j = 0; j < m; ++j) {
-    kn_of(K, d, H->mu_ref, mem[j], fmaxf(mag[j], 1e-12f), kn);
+    kn_of(K, d, mu, mem[j], fmaxf(mag[j], 1e-12f), kn);
     side[j] = canon_dot(kn, b, d) > canon_dot(kn, a, d);
     proj[j] = canon_dot(kn, vs, d);
     n1 += side[j];
@@ -191,6 +182,29 @@ static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {
       side[j] = rank >= half;
     }
   }
+  free(proj); free(kn); free(a); free(b); free(s0); free(s1); free(vs);
+}
+
+static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {
+  const int d = H->d;
+  int* mem = (int*)malloc(sizeof(int) * (size_t)(stop > 0 ? stop : 1));
+  int m = 0;
+  for (int j = 1; j < stop; ++j)
+    if (H->labels[j] == c && m < H->ms) mem[m++] = j;
+  if (m < 2) { free(mem); return; }
+  float* mag = (float*)malloc(sizeof(float) * m);
+  int* side = (int*)malloc(sizeof(int) * m);
+  float* kr = (float*)malloc(sizeof(float) * d);
+  float* a = (float*)malloc(sizeof(float) * d);
+  float* b = (float*)malloc(sizeof(float) * d);
+  float* s0 = (float*)malloc(sizeof(float) * d);
+  float* s1 = (float*)malloc(sizeof(float) * d);
+  for (int j = 0; j < m; ++j) {
+    for (int i = 0; i < d; ++i) kr[i] = K[(int64_t)mem[j] * d + i] - H->mu_ref[i];
+    mag[j] = sqrtf(canon_dot(kr, kr, d));
+  }
+  canon_bisect(K, d, H->mu_ref, mem, mag, m, side);
+  int n1 = 0;
   ordered_sums(K, d, H->mu_ref, mem, mag, side, m, s0, s1, &n1);
   float x0 = 0.f, x1 = 0.f, y0 = INFINITY, y1 = INFINITY;
   for (int j = 0; j < m; ++j) {
@@ -214,7 +228,7 @@ static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {
   H->count[c] = m - n1; H->count[nw] = n1;
   *H->n_c = nw + 1;
   *H->nsplit += 1;
-  free(mem); free(mag); free(proj); free(side); free(kr); free(kn); free(a); free(b); free(s0); free(s1); free(vs);
+  free(mem); free(mag); free(side); free(kr); free(a); free(b); free(s0); free(s1);
 }
 
 /* ---- division after a fit ------------------------------------------------------------------ */
@@ -229,8 +243,10 @@ static void split(canon_head_t* H, const float* K, int c, int nw, int stop) {
  * the slot, part p > 0 takes base + p - 1; a cluster is split when all fit in C. Sums run over
  * members in position order. The int8 copies are left to a refresh. Returns the clusters split;
  * *n_over receives the number of clusters over the cap. */
-#define KMAX 32
-static void kmeans_parts(const float* K, int d, const float* mu, const int* mem, const float* mag, int m, int k,
+/* Cosine k-means of the members into k parts (_kmeans_padded, src/ssa/attn/sphere_gpu.py:56-73):
+ * seeds at members j*m/k, `iters` updates (an empty part keeps its centroid), then the final
+ * assignment; argmax ties to the lowest part. part[j] receives member j's part. */
+void canon_kmeans_parts(const float* K, int d, const float* mu, const int* mem, const float* mag, int m, int k,
                          int iters, int* part) {
   float* cent = (float*)malloc(sizeof(float) * (size_t)k * d);
   float* sums = (float*)malloc(sizeof(float) * (size_t)k * d);
@@ -280,7 +296,8 @@ int canon_split_fit_head(canon_head_t* H, const float* K, int start, int end, fl
   float* mag = (float*)malloc(sizeof(float) * (size_t)(end > 0 ? end : 1));
   float* kr = (float*)malloc(sizeof(float) * d);
   float* kn = (float*)malloc(sizeof(float) * d);
-  float* sums = (float*)malloc(sizeof(float) * (size_t)KMAX * d);
+  float* sums = NULL;
+  int* sizes = NULL; int* renum = NULL; int* slot = NULL;
   for (int i = 0; i < no; ++i) {
     const int c = list[i];
     if ((rank0 + i) % 64 == 0) base = n_cur;
@@ -302,15 +319,17 @@ int canon_split_fit_head(canon_head_t* H, const float* K, int start, int end, fl
     }
     const float kf = ceilf(((float)m * split_factor) / cap_now);
     int k = kf < 2.f ? 2 : (int)kf;
-    if (k > KMAX) k = KMAX;
-    kmeans_parts(K, d, H->mu_ref, mem, mag, m, k, iters, part);
-    int sizes[KMAX], renum[KMAX], nz = 0;
+    canon_kmeans_parts(K, d, H->mu_ref, mem, mag, m, k, iters, part);
+    sums = (float*)realloc(sums, sizeof(float) * (size_t)k * d);
+    sizes = (int*)realloc(sizes, sizeof(int) * (size_t)k);
+    renum = (int*)realloc(renum, sizeof(int) * (size_t)k);
+    slot = (int*)realloc(slot, sizeof(int) * (size_t)k);
+    int nz = 0;
     for (int p = 0; p < k; ++p) sizes[p] = 0;
     for (int j = 0; j < m; ++j) sizes[part[j]] += 1;
     for (int p = 0; p < k; ++p) renum[p] = sizes[p] > 0 ? nz++ : -1;
     const int extra = nz - 1;
     if (extra > 0 && base + extra <= C) {
-      int slot[KMAX];
       for (int p = 0; p < nz; ++p) slot[p] = p == 0 ? c : base + p - 1;
       for (int p = 0; p < nz; ++p) {
         const int s = slot[p];
@@ -339,7 +358,7 @@ int canon_split_fit_head(canon_head_t* H, const float* K, int start, int end, fl
     }
     base += extra > 0 ? extra : 0;
   }
-  free(list); free(mem); free(part); free(mag); free(kr); free(kn); free(sums);
+  free(list); free(mem); free(part); free(mag); free(kr); free(kn); free(sums); free(sizes); free(renum); free(slot);
   return done;
 }
 
@@ -486,15 +505,18 @@ void canon_select(const canon_head_t* H, const float* q, int G, double budget, i
 
 /* ---- prefill ------------------------------------------------------------------------------- */
 
+/* Nearest centroid: argmax of the canonical dot, lowest index on ties; NaN scores never win, and
+ * a key whose every score is NaN (a non-finite key) joins cluster 0, the index torch.argmax
+ * returns on a row of NaNs. */
 static void assign_all(const float* xn, int nb, int d, const float* cent, int nc, int* as) {
   for (int j = 0; j < nb; ++j) {
     float best = 0.f;
     int bi = -1;
     for (int c = 0; c < nc; ++c) {
       float sc = canon_dot(xn + (int64_t)j * d, cent + (int64_t)c * d, d);
-      if (bi < 0 || sc > best) { best = sc; bi = c; }
+      if (sc == sc && (bi < 0 || sc > best)) { best = sc; bi = c; }
     }
-    as[j] = bi;
+    as[j] = bi < 0 ? 0 : bi;
   }
 }
 

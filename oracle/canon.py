@@ -56,6 +56,12 @@ def lib():
                                               ct.c_float, ct.c_int, ct.c_int, ct.c_int, ct.POINTER(ct.c_int)]
         _lib.canon_refresh8.restype = None
         _lib.canon_refresh8.argtypes = [ct.POINTER(HeadC)]
+        _lib.canon_bisect.restype = None
+        _lib.canon_bisect.argtypes = [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int,
+                                      ct.c_void_p]
+        _lib.canon_kmeans_parts.restype = None
+        _lib.canon_kmeans_parts.argtypes = [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int,
+                                            ct.c_int, ct.c_int, ct.c_void_p]
         _lib.canon_build.restype = None
         _lib.canon_build.argtypes = [ct.POINTER(HeadC), ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_int,
                                      ct.c_int, ct.c_int, ct.c_void_p]
@@ -95,6 +101,31 @@ def canon_exp(x: float) -> float:
 
 def canon_q8(u: float) -> int:
     return int(lib().canon_q8(float(u)))
+
+
+def _members(K, mu):
+    K = np.ascontiguousarray(K, dtype=np.float32)
+    m, d = K.shape
+    mu = np.zeros(d, np.float32) if mu is None else np.ascontiguousarray(mu, dtype=np.float32)
+    mem = np.arange(m, dtype=np.int32)
+    mag = np.array([np.float32(np.sqrt(np.float32(canon_dot(K[j] - mu, K[j] - mu)))) for j in range(m)], np.float32)
+    return K, mu, mem, mag
+
+
+def canon_bisect(K, mu=None) -> np.ndarray:
+    """Sides of the bisection of the rows of ``K [m, d]`` (centred by ``mu``; _bisect_padded)."""
+    K, mu, mem, mag = _members(K, mu)
+    side = np.zeros(K.shape[0], np.int32)
+    lib().canon_bisect(_p(K), K.shape[1], _p(mu), _p(mem), _p(mag), K.shape[0], _p(side))
+    return side
+
+
+def canon_kmeans_parts(K, k: int, iters: int, mu=None) -> np.ndarray:
+    """Parts of the cosine k-means division of the rows of ``K [m, d]`` into ``k`` (_kmeans_padded)."""
+    K, mu, mem, mag = _members(K, mu)
+    part = np.zeros(K.shape[0], np.int32)
+    lib().canon_kmeans_parts(_p(K), K.shape[1], _p(mu), _p(mem), _p(mag), K.shape[0], int(k), int(iters), _p(part))
+    return part
 
 
 GROUP_ID = {"sum_share": 0, "per_head": 1, "max": 2, "max_rel": 3}

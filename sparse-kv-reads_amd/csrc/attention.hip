@@ -102,9 +102,25 @@ using namespace ssa;
 
 namespace {
 
+int elem_size(int dt) { return dt == kF32 ? 4 : (dt == kBF16 || dt == kF16) ? 2 : 0; }
+
+// The kernel reads q, K and V rows and the split accumulators as 16-byte vectors (and the
+// accumulators with 8-byte atomic loads): every row it touches must start on a 16-byte boundary.
+bool rows_aligned(const ssa_attn_args_t* x) {
+  const int qe = elem_size(x->q_dtype), ke = elem_size(x->kv_dtype);
+  if (!qe || !ke) return false;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  auto s16 = [](int64_t s, int e) { return (s * e) % 16 == 0; };
+  return a16(x->q) && a16(x->k) && a16(x->v) && a16(x->part_a) && s16(x->s_qh, qe) && s16(x->s_kh, ke) &&
+         s16(x->s_kn, ke) && s16(x->s_vh, ke) && s16(x->s_vn, ke) && (x->d * ke) % 16 == 0;
+}
+
 int launch_decode(const ssa_attn_args_t* x, int mode, void* stream, const ssa_index_state_t* st = nullptr,
                   const ssa_select_args_t* sel = nullptr, const ssa_insert_args_t* ins = nullptr) {
   if (!x || x->G < 1 || x->G > 8 || x->S < 1 || x->S > kMaxS || x->n_heads < 1) return hipErrorInvalidValue;
+  if (!x->q || !x->k || !x->v || !x->out || !x->part_m || !x->part_l || !x->part_a || !x->part_cnt || !x->counter)
+    return hipErrorInvalidValue;
+  if (!rows_aligned(x)) return hipErrorInvalidValue;
   if (mode == kLabelled && (x->w_len < 1 || x->w_len > kMaxW)) return hipErrorInvalidValue;
   DecodeParams p{};
   p.q = x->q; p.s_qh = x->s_qh; p.q_dtype = x->q_dtype;

@@ -404,7 +404,9 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
     const int j = j0 + lane;
     if (j < A.nb) {
       const int k = kcnt[wave][lane];
-      const int c = k == 0 ? -1 : (k == 1 && !flushed) ? kfirst[wave][lane] : (int)(unsigned int)rk[wave][lane];
+      // no candidate: every score of the key is NaN (a non-finite key); it joins cluster 0, the
+      // first index, as torch.argmax picks on a row of NaNs
+      const int c = k == 0 ? 0 : (k == 1 && !flushed) ? kfirst[wave][lane] : (int)(unsigned int)rk[wave][lane];
       A.b.assign[(int64_t)s * A.nb + j] = c;
       if (write_labels) A.st.labels[(int64_t)h * A.st.capacity + A.b.start + j] = (int16_t)c;
     }
@@ -453,6 +455,7 @@ __global__ __launch_bounds__(kT) void block_sum_kernel(BuildArgs A, int ncl, int
     for (int r = tid; r < nk; r += kT) {
       const int c = s_as[r];
       const int bits = __float_as_int(mg[r]);   // lengths are >= 0, so int order is float order
+      if (mg[r] != mg[r]) continue;             // a NaN length is ignored, as fmaxf / fminf do
       atomicMax(reinterpret_cast<int*>(A.st.mmax + (int64_t)h * A.st.C + c), bits);
       atomicMin(reinterpret_cast<int*>(A.st.mmin + (int64_t)h * A.st.C + c), bits);
     }

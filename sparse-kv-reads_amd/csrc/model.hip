@@ -419,8 +419,12 @@ __global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const T* __res
   if (tid != 0) return;
   for (int w = 1; w < kArgThreads / 64; ++w)
     if (arg_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
-  // the returning max completes at the coherence point before this workgroup counts itself in
+  // The max must have completed at the coherence point before this workgroup counts itself in:
+  // both atomics are relaxed and go to different addresses, so nothing else orders them. The
+  // asm wait is a hardware wait for every outstanding memory operation of this thread (the
+  // atomic included) and, through its memory clobber, a compiler barrier.
   if (bi < N) (void)__hip_atomic_fetch_max(key + r, arg_key(bv, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const unsigned int old = __hip_atomic_fetch_add(cnt + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (old != (unsigned int)(P - 1)) return;
   const unsigned long long k = __hip_atomic_load(key + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -60,7 +60,31 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, "-shared", f"--offload-arch={ARCH}", *objs, "-o", str(tmp)])
     os.replace(tmp, LIB)
+    _write_build_info(hipcc)
     return LIB
+
+
+def _write_build_info(hipcc: str) -> None:
+    """Record the source revision the library was built from (read by ``ssa_amd.stamp`` where
+    the tree has no git metadata)."""
+    import json
+    import time
+    root = str(PKG.parents[1])
+    try:
+        rev = {"sha": subprocess.check_output(["git", "-C", root, "rev-parse", "HEAD"], text=True,
+                                              stderr=subprocess.DEVNULL).strip(),
+               "dirty": bool(subprocess.check_output(["git", "-C", root, "status", "--porcelain",
+                                                      "--untracked-files=no"], text=True,
+                                                     stderr=subprocess.DEVNULL).strip())}
+    except (OSError, subprocess.CalledProcessError):
+        rev = {"sha": "nogit"}
+    try:
+        ver = subprocess.run([hipcc, "--version"], capture_output=True, text=True).stdout.splitlines()[0]
+    except (OSError, IndexError):
+        ver = hipcc
+    (PKG / "BUILD_INFO.json").write_text(json.dumps({"git_sha": rev.get("sha"), "dirty": rev.get("dirty"), "arch": ARCH,
+                                      "built_at": time.strftime("%Y-%m-%dT%H:%M:%SZ", time.gmtime()),
+                                      "hipcc": ver}) + "\n")
 
 
 if __name__ == "__main__":

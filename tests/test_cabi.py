@@ -84,3 +84,30 @@ def test_glue_entry_points_refuse_bad_arguments_before_any_launch():
     assert h.ssa_argmax_rows(fake, fake, 0, 100, 1, fake, None) != 0
     assert h.ssa_embed_rmsnorm(None, fake, fake, fake, fake, 2, 64, 10, 1e-6, fake, fake, 1, None) != 0
     assert h.ssa_embed_rmsnorm(fake, fake, fake, fake, fake, 2, 64, 10, 1e-6, None, fake, 1, None) != 0
+
+
+def test_attention_refuses_misaligned_rows_before_any_launch():
+    """q, K, V and the split accumulators are read as 16-byte vectors: a 4-byte-aligned part_a
+    (or row stride) is refused with hipErrorInvalidValue (1) before anything is launched."""
+    h = _lib_handle()
+    base = 1 << 20                                       # 16-byte aligned; never dereferenced
+
+    def args(**kw):
+        a = _lib.AttnArgs()
+        a.q, a.s_qh, a.q_dtype = base, 128, 1
+        a.k, a.s_kh, a.s_kn = base, 128 * 64, 128
+        a.v, a.s_vh, a.s_vn = base, 128 * 64, 128
+        a.kv_dtype = 1
+        a.part_m, a.part_l, a.part_a, a.part_cnt, a.counter = base, base, base, base, base
+        a.out, a.s_oh, a.out_dtype = base, 128, 1
+        a.n_heads, a.G, a.d, a.S, a.n_host = 2, 2, 128, 4, 64
+        a.labels, a.s_lh, a.w, a.s_wr, a.w_len = base, 64, base, 17, 17
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+    for bad in (dict(part_a=base + 4), dict(q=base + 2), dict(k=base + 8), dict(s_kn=124), dict(s_qh=36),
+                dict(part_a=None), dict(counter=None)):
+        a = args(**bad)
+        assert h.ssa_label_attention(ct.byref(a), None) == 1, bad
+        assert h.ssa_dense_attention(ct.byref(a), None) == 1, bad

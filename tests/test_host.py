@@ -112,3 +112,33 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=300)
     assert r.returncode == 2
     assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_provenance_stamp_has_the_reference_fields():
+    """src/ssa/harness/stamp.py:35-45: revision, torch version, python, platform, GPU."""
+    from ssa_amd.stamp import stamp
+    s = stamp({"x": 1})
+    for k in ("git_sha", "torch_version", "hip_version", "python_version", "platform", "gpu", "x"):
+        assert k in s
+    assert s["git_sha"] and s["git_sha"] != "nogit"
+
+
+def test_cpu_baseline_path_matches_the_numpy_oracle():
+    """oracle/torch_ref.py (the timed CPU baseline) selects the same clusters as the numpy
+    restatement and attends over every key to the same output."""
+    import numpy as np
+    import torch
+    from oracle.reference import SphereIndexRef
+    from oracle.torch_ref import SphereIndexTorch
+    from ssa_amd.sphere_fused import kmeans_init_indices
+    from ssa_amd.synth import make_cache
+    K, V, q, _ = make_cache(1, 2, 700, 32, H=4, centers=16, seed=3, dtype=torch.float32)
+    K, V, q = K[0].contiguous(), V[0].contiguous(), q[0].contiguous()
+    t = SphereIndexTorch(C=16, window=16, init_indices=lambda m, c: kmeans_init_indices(m, c, 0))
+    r = SphereIndexRef(C=16, window=16, init_indices=lambda m, c, s: kmeans_init_indices(m, c, s).numpy())
+    for n in (640, 641, 642):
+        out_t, lab_t, w_t = t.attend(q, K, V, n=n, budget=0.3)
+        out_r, lab_r, w_r = r.attend(q.numpy(), K.numpy(), V.numpy(), n=n, budget=0.3)
+        assert np.array_equal(lab_t.numpy(), lab_r)
+        assert np.array_equal(w_t.numpy(), w_r)
+        assert np.abs(out_t.numpy() - out_r).max() < 1e-4
