@@ -154,6 +154,24 @@ int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const 
 int ssa_sparse_step(const ssa_index_state_t* st, const ssa_select_args_t* sel, const ssa_attn_args_t* args,
                     const ssa_insert_args_t* ins_ahead, void* stream);
 
+/* Bytes of the split workspace held by the library for ssa_sparse_step_noalloc, per GPU. */
+#define SSA_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/* ssa_sparse_step without caller-supplied split buffers: no counterpart in the reference. It is
+ * for callers that cannot allocate device memory (code under graph capture, serving loops,
+ * harnesses that forbid hipMalloc). args->part_m, part_l, part_a, part_cnt and counter are
+ * ignored (they may be NULL): the arrival counters and split partials live in a device array of
+ * SSA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, kept until the process ends. The
+ * call allocates nothing; it enqueues a small kernel that clears the counters, then the step.
+ * Layout, 256-byte aligned each: counters [Hk] int32, rows read [Hk, S] int32, m and l
+ * [Hk, S, G] fp32, a [Hk, S, G, d] fp32; returns hipErrorInvalidValue before any launch when
+ * they exceed SSA_NOALLOC_SCRATCH_BYTES (e.g. Hk = 8, S = 32, G = 2, d = 128 takes 0.27 MB).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, or
+ * two graphs replayed concurrently) race, and must be serialised by the caller. The stream must
+ * belong to the current device. Otherwise as ssa_sparse_step. */
+int ssa_sparse_step_noalloc(const ssa_index_state_t* st, const ssa_select_args_t* sel, const ssa_attn_args_t* args,
+                            const ssa_insert_args_t* ins_ahead, void* stream);
+
 /* ---- prefill: fit, bin and summarise the prompt's keys ------------------------------------- */
 
 typedef struct ssa_build_args {

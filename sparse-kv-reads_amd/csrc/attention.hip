@@ -1,6 +1,8 @@
 // C ABI of the attention entry points, and the standalone merge and compaction kernels of the
 // reference's functional API. The decode kernel itself is in decode.h, instantiated once per KV
 // dtype by decode_bf16.hip, decode_f16.hip and decode_f32.hip.
+#include <mutex>
+
 #include "decode.h"
 
 namespace ssa {
@@ -93,6 +95,19 @@ __global__ __launch_bounds__(256) void compact_place_kernel(const int16_t* label
   }
 }
 
+// Clears n int32 values (the arrival counters of the no-alloc step): a kernel rather than a
+// memset, so that a captured graph holds no memset node.
+__global__ __launch_bounds__(256) void zero_i32_kernel(int32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += 256) p[i] = 0;
+}
+
+// Split workspace of ssa_sparse_step_noalloc: the arrival counters and split partials of one
+// launch, in this file-scope device array instead of caller-supplied buffers. Each GPU the
+// library runs on holds its own copy until the process ends. Host code never passes the array's
+// name to a kernel (on the host it is a stand-in, not a device address): its device address is
+// looked up once per device with hipGetSymbolAddress and kept in noalloc_base below.
+static __device__ __align__(256) unsigned char scratch[SSA_NOALLOC_SCRATCH_BYTES];
+
 }  // namespace ssa
 
 // ---------------------------------------------------------------------------------------------
@@ -115,8 +130,11 @@ bool rows_aligned(const ssa_attn_args_t* x) {
          s16(x->s_kn, ke) && s16(x->s_vh, ke) && s16(x->s_vn, ke) && (x->d * ke) % 16 == 0;
 }
 
+// zero_first: arrival counters to clear (a fill kernel on the same stream) once the arguments
+// have been checked and before the decode kernel is launched; nullptr for none.
 int launch_decode(const ssa_attn_args_t* x, int mode, void* stream, const ssa_index_state_t* st = nullptr,
-                  const ssa_select_args_t* sel = nullptr, const ssa_insert_args_t* ins = nullptr) {
+                  const ssa_select_args_t* sel = nullptr, const ssa_insert_args_t* ins = nullptr,
+                  int32_t* zero_first = nullptr) {
   if (!x || x->G < 1 || x->G > 8 || x->S < 1 || x->S > kMaxS || x->n_heads < 1) return hipErrorInvalidValue;
   if (!x->q || !x->k || !x->v || !x->out || !x->part_m || !x->part_l || !x->part_a || !x->part_cnt || !x->counter)
     return hipErrorInvalidValue;
@@ -158,12 +176,65 @@ int launch_decode(const ssa_attn_args_t* x, int mode, void* stream, const ssa_in
     }
   }
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  if (zero_first) {
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(256), 0, hs, zero_first, x->n_heads);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   switch (x->kv_dtype) {
     case kBF16: return launch_decode_bf16(p, x->d, mode, hs);
     case kF16: return launch_decode_f16(p, x->d, mode, hs);
     case kF32: return launch_decode_f32(p, x->d, mode, hs);
   }
   return hipErrorInvalidValue;
+}
+
+// Byte offsets of the split workspace's arrays in the scratch array, each on a 256-byte boundary.
+struct NoAllocLayout {
+  size_t counter, part_cnt, part_m, part_l, part_a, total;
+};
+
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+NoAllocLayout noalloc_layout(int n_heads, int S, int G, int d) {
+  const size_t hs = (size_t)n_heads * (size_t)S, hsg = hs * (size_t)G;
+  NoAllocLayout L;
+  L.counter = 0;
+  L.part_cnt = round256(sizeof(int32_t) * (size_t)n_heads);
+  L.part_m = L.part_cnt + round256(sizeof(int32_t) * hs);
+  L.part_l = L.part_m + round256(sizeof(float) * hsg);
+  L.part_a = L.part_l + round256(sizeof(float) * hsg);
+  L.total = L.part_a + round256(sizeof(float) * hsg * (size_t)d);
+  return L;
+}
+
+// Device address of this device's scratch array, looked up on the first call made with the
+// device current and kept per device.
+constexpr int kMaxDevices = 64;
+std::mutex noalloc_mu;
+void* noalloc_base[kMaxDevices];
+
+hipError_t noalloc_scratch(hipStream_t stream, unsigned char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return e;
+    if (sdev != dev) return hipErrorInvalidValue;     // the stream must belong to the current device
+  }
+  std::lock_guard<std::mutex> lock(noalloc_mu);
+  if (!noalloc_base[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    noalloc_base[dev] = p;
+  }
+  *out = static_cast<unsigned char*>(noalloc_base[dev]);
+  return hipSuccess;
 }
 
 }  // namespace
@@ -179,6 +250,27 @@ extern "C" int ssa_dense_attention(const ssa_attn_args_t* args, void* stream) {
 extern "C" int ssa_sparse_step(const ssa_index_state_t* st, const ssa_select_args_t* sel, const ssa_attn_args_t* args,
                                const ssa_insert_args_t* ins_ahead, void* stream) {
   return launch_decode(args, kFused, stream, st, sel, ins_ahead);
+}
+
+extern "C" int ssa_sparse_step_noalloc(const ssa_index_state_t* st, const ssa_select_args_t* sel,
+                                       const ssa_attn_args_t* args, const ssa_insert_args_t* ins_ahead,
+                                       void* stream) {
+  if (!args || args->n_heads < 1 || args->S < 1 || args->S > kMaxS || args->G < 1 || args->G > 8 || args->d < 1)
+    return hipErrorInvalidValue;
+  const NoAllocLayout L = noalloc_layout(args->n_heads, args->S, args->G, args->d);
+  if (L.total > (size_t)SSA_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;   // beyond the scratch array
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  unsigned char* base = nullptr;
+  const hipError_t e = noalloc_scratch(hs, &base);
+  if (e != hipSuccess) return e;
+  ssa_attn_args_t x = *args;
+  x.counter = reinterpret_cast<int32_t*>(base + L.counter);
+  x.part_cnt = reinterpret_cast<int32_t*>(base + L.part_cnt);
+  x.part_m = reinterpret_cast<float*>(base + L.part_m);
+  x.part_l = reinterpret_cast<float*>(base + L.part_l);
+  x.part_a = reinterpret_cast<float*>(base + L.part_a);
+  // the counters are cleared by every call: the array keeps whatever the last call left in it
+  return launch_decode(&x, kFused, stream, st, sel, ins_ahead, x.counter);
 }
 
 extern "C" int ssa_merge_splits(const float* m, const float* l, const float* a, int64_t s_mh, int64_t s_ms,

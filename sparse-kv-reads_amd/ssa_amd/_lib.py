@@ -110,6 +110,8 @@ ENTRY_POINTS = {
     "ssa_split_fit": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SplitArgs), vp]),
     "ssa_sparse_step": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs),
                                    ct.POINTER(InsertArgs), vp]),
+    "ssa_sparse_step_noalloc": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs),
+                                           ct.POINTER(InsertArgs), vp]),
     "ssa_rmsnorm_add": (ct.c_int, [vp, vp, vp, vp, ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32, vp]),
     "ssa_qk_norm_rope_cache": (ct.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, ct.c_int32, ct.c_int32,
                                           ct.c_int32, ct.c_int32, ct.c_float, ct.c_int32, vp]),

@@ -111,3 +111,16 @@ def test_attention_refuses_misaligned_rows_before_any_launch():
         a = args(**bad)
         assert h.ssa_label_attention(ct.byref(a), None) == 1, bad
         assert h.ssa_dense_attention(ct.byref(a), None) == 1, bad
+
+
+def test_noalloc_step_refuses_a_workspace_beyond_its_array_before_any_call():
+    """ssa_sparse_step_noalloc checks the split workspace against SSA_NOALLOC_SCRATCH_BYTES (4 MiB)
+    first: an oversized one returns hipErrorInvalidValue (1) before any HIP call."""
+    h = _lib_handle()
+    text = HEADER.read_text()
+    assert re.search(r"#define SSA_NOALLOC_SCRATCH_BYTES \(4u << 20\)", text)
+    a = _lib.AttnArgs()
+    a.n_heads, a.G, a.d, a.S = 64, 8, 256, 32            # 64 * 32 * 8 * 256 * 4 B = 16 MiB of partials
+    assert h.ssa_sparse_step_noalloc(None, None, ct.byref(a), None, None) == 1
+    a.n_heads, a.G, a.d, a.S = 8, 2, 128, 300            # more splits than a head takes
+    assert h.ssa_sparse_step_noalloc(None, None, ct.byref(a), None, None) == 1
