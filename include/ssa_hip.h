@@ -210,8 +210,12 @@ typedef struct ssa_split_args {
   int32_t* mem; int32_t* side; float* proj; float* smag;   /* scratch [n_sel, ms] */
   int32_t ms;                /* members held per cluster (at least the largest cluster) */
   int32_t* over;             /* [n_sel] out: clusters over the cap at the start of the round */
-  int32_t* done;             /* [n_sel] out: clusters divided in the round (-1: more than 32 parts asked) */
+  int32_t* done;             /* [n_sel] out: clusters divided in the round (-1: a division into more
+                                than 32 parts found no room in parts, or asked for more than 1024) */
   int32_t refresh_only;      /* 1: only rebuild the int8 copies of the heads (after the last round) */
+  float* parts;              /* scratch [n_sel, 2, max_parts, d] for k-means divisions into more than 32
+                                parts (up to 32 are held on chip); NULL if none is expected */
+  int32_t max_parts;         /* rows of parts per head, at most 1024 */
 } ssa_split_args_t;
 
 /* One round of the division of clusters over their cap after a k-means fit: the clusters with

@@ -530,7 +530,8 @@ __global__ __launch_bounds__(kT) void refresh8_kernel(BuildArgs A) {
 // workgroup per head takes that head's clusters over the cap in slot order, one at a time, so
 // the spare slots are handed out in the reference's order.
 
-constexpr int kKmax = 32;     // parts of one k-means division
+constexpr int kKmax = 32;     // parts of one k-means division held in LDS; more use a->parts
+constexpr int kMaxParts = kMaxC;
 
 struct FitArgs {
   ssa_index_state_t st;
@@ -540,8 +541,8 @@ struct FitArgs {
 struct FitSmem : InsertBase {
   float cent[kKmax][kMaxD];
   float sums[kKmax][kMaxD];
-  float pmx[kKmax], pmn[kKmax];
-  int cntp[kKmax], renum[kKmax], slot[kKmax];
+  float pmx[kMaxParts], pmn[kMaxParts];
+  int cntp[kMaxParts], renum[kMaxParts], slot[kMaxParts];
   int list[kMaxC];
   int nlist, nz, bad;
   union {
@@ -574,12 +575,20 @@ __global__ __launch_bounds__(kT) void fit_count_kernel(FitArgs A) {
   }
 }
 
-// S.sums[p] = ordered sum (members in position order) of the unit directions of the members in
+// Rows of the parts' centroids and sums: in LDS for up to kKmax parts, else in the caller's
+// scratch (a->parts, [2, max_parts, d] per head); row p of each starts at p * stride.
+struct PartRows {
+  float* cent; float* sums; int stride;
+  __device__ float* c(int p) const { return cent + (int64_t)p * stride; }
+  __device__ float* s(int p) const { return sums + (int64_t)p * stride; }
+};
+
+// P.s(p) = ordered sum (members in position order) of the unit directions of the members in
 // part p (H.side), S.cntp[p] their number, for p < k.
-__device__ __forceinline__ void fit_sums(FitSmem& S, const Head& H, const Keys& K, int m, int k) {
+__device__ __forceinline__ void fit_sums(FitSmem& S, const PartRows& P, const Head& H, const Keys& K, int m, int k) {
   const int tid = threadIdx.x, d = H.d;
-  for (int e = tid; e < k * d; e += kT) S.sums[e / d][e % d] = 0.f;
-  if (tid < k) S.cntp[tid] = 0;
+  for (int e = tid; e < k * d; e += kT) P.s(e / d)[e % d] = 0.f;
+  for (int p = tid; p < k; p += kT) S.cntp[p] = 0;
   __syncthreads();
   // member tiles as in member_sums; the next tile's keys load while this one is summed
   const bool v16 = keys_vec16(K);
@@ -595,7 +604,8 @@ __device__ __forceinline__ void fit_sums(FitSmem& S, const Head& H, const Keys& 
     if (tid < d)
       for (int r = 0; r < nr; ++r) {
         const int p = S.u.spl.tside[r];
-        S.sums[p][tid] = S.sums[p][tid] + S.u.spl.tile[r * d + tid];
+        float* sp = P.s(p) + tid;
+        *sp = *sp + S.u.spl.tile[r * d + tid];
       }
     if (tid == kT - 1)
       for (int r = 0; r < nr; ++r) S.cntp[S.u.spl.tside[r]] += 1;
@@ -606,12 +616,13 @@ __device__ __forceinline__ void fit_sums(FitSmem& S, const Head& H, const Keys& 
 // Cosine k-means of the m members into k parts (_kmeans_padded): centroids start at members
 // j*m/k, `iters` updates (a part with members takes the unit of its ordered sum), then a final
 // assignment; each member's part (the best canonical dot, lowest part on ties) goes to H.side.
-__device__ __forceinline__ void fit_kmeans(FitSmem& S, const Head& H, const Keys& K, int m, int k, int iters) {
+__device__ __forceinline__ void fit_kmeans(FitSmem& S, const PartRows& P, const Head& H, const Keys& K, int m, int k,
+                                           int iters) {
   const int tid = threadIdx.x, d = H.d;
   for (int e = tid; e < k * d; e += kT) {
     const int p = e / d, i = e % d;
     const int j = min((int)(((int64_t)p * m) / k), m - 1);
-    S.cent[p][i] = (K(H.mem[j], i) - S.mu[i]) / fmaxf(H.smag[j], 1e-12f);
+    P.c(p)[i] = (K(H.mem[j], i) - S.mu[i]) / fmaxf(H.smag[j], 1e-12f);
   }
   __syncthreads();
   for (int it = 0; it <= iters; ++it) {
@@ -620,18 +631,20 @@ __device__ __forceinline__ void fit_kmeans(FitSmem& S, const Head& H, const Keys
       const float magc = fmaxf(H.smag[j], 1e-12f);
       auto kn = [&](int i) { return (K(pos, i) - S.mu[i]) / magc; };
       int best = 0;
-      float bs = cdot_rolled(kn, [&](int i) { return S.cent[0][i]; }, d);
+      const float* c0 = P.c(0);
+      float bs = cdot_rolled(kn, [&](int i) { return c0[i]; }, d);
       for (int p = 1; p < k; ++p) {
-        const float sc = cdot_rolled(kn, [&](int i) { return S.cent[p][i]; }, d);
+        const float* cp = P.c(p);
+        const float sc = cdot_rolled(kn, [&](int i) { return cp[i]; }, d);
         if (sc > bs) { bs = sc; best = p; }
       }
       H.side[j] = best;
     }
     __syncthreads();
     if (it == iters) break;
-    fit_sums(S, H, K, m, k);
+    fit_sums(S, P, H, K, m, k);
     for (int p = 0; p < k; ++p)
-      if (S.cntp[p] > 0) block_unit(S, S.sums[p], S.cent[p], d);
+      if (S.cntp[p] > 0) block_unit(S, P.s(p), P.c(p), d);
   }
 }
 
@@ -695,13 +708,20 @@ __global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
     }
     __syncthreads();
     const float kf = ceilf(((float)m * a.split_factor) / cap);
-    int k = kf < 2.f ? 2 : (int)kf;
+    int k = kf < 2.f ? 2 : (kf >= (float)kMaxParts ? kMaxParts + 1 : (int)kf);
+    PartRows P{&S.cent[0][0], &S.sums[0][0], kMaxD};
     if (k > kKmax) {
-      k = kKmax;
-      if (tid == 0) S.bad = 1;
+      if (!a.parts || k > a.max_parts || k > kMaxParts) {
+        // no room for the parts: the cluster is left whole and the round reports it (done = -1)
+        if (tid == 0) S.bad = 1;
+        __syncthreads();
+        continue;
+      }
+      float* base_p = a.parts + (int64_t)s * 2 * a.max_parts * D;
+      P = PartRows{base_p, base_p + (int64_t)a.max_parts * D, D};
     }
-    fit_kmeans(S, H, K, m, k, a.iters);
-    fit_sums(S, H, K, m, k);                              // final parts: ordered sums and sizes
+    fit_kmeans(S, P, H, K, m, k, a.iters);
+    fit_sums(S, P, H, K, m, k);                           // final parts: ordered sums and sizes
     if (tid == 0) {
       int nz = 0;
       for (int p = 0; p < k; ++p) S.renum[p] = S.cntp[p] > 0 ? nz++ : -1;
@@ -721,8 +741,8 @@ __global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
         const int q = S.renum[p];
         if (q < 0) continue;
         const int row = S.slot[q];
-        if (tid < D) H.sum_dir[(int64_t)row * D + tid] = S.sums[p][tid];
-        block_unit(S, S.sums[p], H.cent + (int64_t)row * D, D);
+        if (tid < D) H.sum_dir[(int64_t)row * D + tid] = P.s(p)[tid];
+        block_unit(S, P.s(p), H.cent + (int64_t)row * D, D);
         if (tid == 0) {
           H.mmax[row] = S.pmx[q];
           H.mmin[row] = S.pmn[q];

@@ -91,7 +91,8 @@ class SplitArgs(ct.Structure):
                 ("mem", vp), ("side", vp), ("proj", vp), ("smag", vp),
                 ("ms", i32),
                 ("over", vp), ("done", vp),
-                ("refresh_only", i32)]
+                ("refresh_only", i32),
+                ("parts", vp), ("max_parts", i32)]
 
 
 # (name, restype, argtypes) of every exported entry point; the C-ABI test checks this list

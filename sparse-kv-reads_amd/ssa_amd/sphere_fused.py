@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from ._lib import (STAGE_WORDS, BuildArgs, IndexState, InsertArgs, SelectArgs, SplitArgs, check, dtype_tag, lib,
@@ -280,6 +281,17 @@ class SphereIndexFused:
         a.iters = self.kmeans_iters
         a.mem, a.side, a.proj, a.smag, a.ms = mem.data_ptr(), side.data_ptr(), proj.data_ptr(), smag.data_ptr(), ms
         a.over, a.done = over.data_ptr(), done.data_ptr()
+        # the k-means round divides a cluster of m keys into max(2, ceil(m * split_factor / cap))
+        # parts (no upper limit, as in the reference); up to 32 parts are held on chip, more in
+        # this scratch, sized for the largest cluster against the smallest cap (float32, as the
+        # kernel computes it)
+        cap_now = np.maximum(np.float32(self.cap.min().item()), np.float32(a.cap_min))
+        k_max = int(np.ceil(np.float32(ms) * np.float32(self.split_factor) / cap_now)) if cap_now > 0 else 2
+        parts = None
+        if k_max > 32:
+            a.max_parts = min(k_max + 1, 1024)
+            parts = torch.empty(H_kv, 2, a.max_parts, self.d, dtype=torch.float32, device=dev)
+            a.parts = parts.data_ptr()
         st = self._state()
         nmeans = True
         while True:
@@ -287,7 +299,7 @@ class SphereIndexFused:
             check(lib().ssa_split_fit(st, a, stream_ptr(dev)), "ssa_split_fit")
             n_over, n_done = int(over.sum()), done.cpu()                  # host sync
             if bool((n_done < 0).any()):
-                raise RuntimeError("a cluster would be divided into more than 32 parts by the post-fit k-means")
+                raise RuntimeError("a cluster would be divided into more than 1024 parts by the post-fit k-means")
             if n_over == 0 or (int(n_done.sum()) == 0 and not nmeans):
                 break
             nmeans = False

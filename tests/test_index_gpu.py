@@ -203,6 +203,34 @@ def test_post_fit_division_is_bit_exact(summary_bits):
     assert np.array_equal(w.cpu().numpy(), canon.select(q, budget=0.2))
 
 
+def test_post_fit_division_into_more_than_64_parts():
+    """A cap far below the fitted clusters' sizes (cap_keys = 10 against ~370 keys per cluster):
+    the k-means round divides each cluster into max(2, ceil(m * split_factor / cap)) >= 64 parts,
+    beyond the 32 held on chip, so the parts' centroids and sums live in the caller's scratch.
+    Same state as the oracle, which has no limit on the parts (src/ssa/attn/sphere_gpu.py:56-73,
+    357-358), and the following insertions and selection agree too."""
+    K, V, q = _keys(2, 3100, H=4, seed=23, centers=8)
+    n = 3000
+    idx = _fused(C=1024, C_init=8, cap_keys=10.0, capacity=4096)
+    idx.observe(K, n)
+    canon = _canon_like(idx, K, n)
+    end = n - idx.window
+    canon.cap[:] = np.float32(10.0)
+    fitted = canon.count.copy()
+    assert math.ceil(int(fitted.max()) * 2.0 / 10.0) >= 64
+    rounds = canon.split_after_fit(K, start=1, end=end, split_factor=idx.split_factor, iters=idx.kmeans_iters)
+    _same(idx, canon)
+    assert rounds >= 1 and int(canon.n_c.min()) > 8 * 32
+    for h in range(2):
+        assert np.array_equal(np.bincount(canon.labels[h, 1:end], minlength=1024), canon.count[h])
+    for m in range(n + 1, n + 20):
+        idx.observe(K, m)
+        canon.insert(K, m, window=16, delta=math.inf)
+    _same(idx, canon)
+    w = idx.labels_and_weights(q, n=n + 19, budget=0.2)[1]
+    assert np.array_equal(w.cpu().numpy(), canon.select(q, budget=0.2))
+
+
 def test_end_to_end_config0_step():
     """Config 0: fp32, 16 query / 8 KV heads, d=128, n=4096, 256 clusters, 10 k-means iterations,
     20% budget: labels, selection and selected indices bit-exact; output within 1e-5."""

@@ -27,7 +27,7 @@ import numpy as np
 import pytest
 
 from oracle import reference as ref
-from oracle.canon import CanonIndex, canon_dot, canon_exp, canon_q8
+from oracle.canon import CanonIndex, canon_dot, canon_exp, canon_kmeans_parts, canon_q8
 
 
 # ---- canonical arithmetic ------------------------------------------------------------------
@@ -408,3 +408,17 @@ def test_post_fit_kmeans_round_finds_obvious_parts():
     n_c = int(c.n_c[0])
     assert set.union(*groups) == set(range(n_c)) and 3 <= n_c <= 6
     assert np.all(c.count[0, :n_c] <= per)
+
+
+def test_kmeans_division_into_70_parts_recovers_70_groups():
+    """The k-means division has no limit on the parts (src/ssa/attn/sphere_gpu.py:357-358): 70
+    tight groups of 10 members around distinct directions, members in group order, k = 70 parts
+    seeded at members j * m / k = 10 j (one per group): every part is exactly one group. A
+    division capped at 32 parts, or seeded elsewhere, could not give this."""
+    d, per, k = 128, 10, 70
+    g = np.random.default_rng(7)
+    dirs = g.standard_normal((k, d))
+    dirs /= np.linalg.norm(dirs, axis=1, keepdims=True)
+    K = np.concatenate([5.0 * dirs[i] + 0.01 * g.standard_normal((per, d)) for i in range(k)]).astype(np.float32)
+    part = canon_kmeans_parts(K, k, 10, mu=np.zeros(d, np.float32))
+    assert np.array_equal(part, np.repeat(np.arange(k), per))
