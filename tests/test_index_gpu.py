@@ -22,7 +22,7 @@ from oracle import reference as ref
 pytestmark = pytest.mark.gpu
 
 FIELDS = ("n_c", "sum_dir", "dir8", "cent", "cent8", "mmax", "mmin", "count", "ksum", "mu_ref", "rbar", "end",
-          "nsplit", "labels")
+          "nsplit", "labels", "flags")
 
 
 def _keys(H_kv, n, d=128, *, H=None, seed=0, dtype=torch.bfloat16, centers=64):
@@ -134,6 +134,34 @@ def test_insertion_is_bit_exact(summary_bits):
     _same(idx, canon)
     counts = np.stack([np.bincount(canon.labels[h, 1:canon.end[h]], minlength=64) for h in range(4)])
     assert np.array_equal(counts, canon.count)
+
+
+@pytest.mark.parametrize("delta", [0.02, 0.2])
+def test_insertion_drift_flags_are_bit_exact(delta):
+    """The flags the insertion kernel sets (src/ssa/kernels/sphere_fused.py:223-227), step by
+    step: bit 0 when |ksum / nb - mu_ref| > delta * rbar, on keys whose mean moves away from the
+    fitted one; bit 1 once a head's cluster count, grown by in-kernel splits, reaches reset_at.
+    The host never acts on the flags here (check_every is huge), so GPU and oracle see the same
+    keys."""
+    K, V, q = _keys(4, 1800, seed=13, centers=16)
+    drift = torch.zeros_like(K)
+    drift[:, 1000:, :8] = 3.0                                  # keys after the fit lean one way
+    K = (K.float() + drift.float()).to(K.dtype)
+    idx = _fused(C=64, C_init=16, delta=delta, check_every=10 ** 9, reset_at=20)
+    idx.observe(K, 1000)
+    canon = _canon_like(idx, K, 1000)
+    cap = float(1.5 * (1000 - 17) / 16)
+    idx.cap.fill_(cap)
+    canon.cap[:] = cap
+    seen = set()
+    for n in range(1001, 1800, 9):
+        idx.observe(K, n)
+        canon.insert(K, n, window=16, delta=delta, reset_at=20)
+        _same(idx, canon, fields=("flags", "end", "ksum", "count", "n_c"))
+        seen |= set(np.unique(canon.flags).tolist())
+    _same(idx, canon)
+    assert seen & {1, 3}, "some head should drift"
+    assert seen & {2, 3} and int(canon.n_c.max()) >= 20, "some head should reach reset_at"
 
 
 @pytest.mark.parametrize("group", ["sum_share", "per_head", "max", "max_rel"])
@@ -277,7 +305,7 @@ def test_fused_step_shapes_match_the_oracle(H, H_kv, d, dtype, group):
     np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=tol)
 
 
-@pytest.mark.parametrize("budget", [0.2, 0.05])
+@pytest.mark.parametrize("budget", [0.4, 0.2, 0.1, 0.05])
 def test_config1_full_size_selection_and_output(budget):
     """configs[1] at its full size (B=1, 16 q / 8 kv heads, d=128, bf16, n=32768, 256 k-means
     clusters, window 64) through the fused step. The 10-iteration fit at 32k is too slow for the
