@@ -229,6 +229,46 @@ typedef struct ssa_split_args {
  * (src/ssa/kernels/sphere_fused.py:411-413). */
 int ssa_split_fit(const ssa_index_state_t* st, const ssa_split_args_t* a, void* stream);
 
+/* ---- maintenance on the device: recentring, reset and refit ------------------------------- */
+
+#define SSA_MAINT_PLAN_WORDS 8   /* header words of the plan, before its 3 * n_heads list words */
+
+typedef struct ssa_maint_args {
+  const void* k; int32_t k_dtype; int64_t s_kh; int64_t s_kn;   /* the layer's cache [Hk, capacity, d] */
+  int32_t refit_all;         /* 1: refit every head (refit_every); 0: act on the flags */
+  int32_t refit;             /* 1: refit the heads whose flag has bit 1 (with refit_all: every head);
+                                0: bit 1 is cleared and ignored (no reset threshold) */
+  int32_t C_init, iters, seed;   /* the fit's clusters, k-means updates, seed of its seed members */
+  float split_factor;        /* > 0: the refit sets cap and divides clusters over it */
+  float cap_keys;            /* > 0: the refit's cap, else split_factor * nb / C_init */
+  double capk;               /* cap floor of the division: max(cap, capk * nb) */
+  int32_t max_heads;         /* heads per build pass (rows of xn, mag, sq, assign, part, part_cnt) */
+  int32_t* plan;             /* [SSA_MAINT_PLAN_WORDS + 3 * Hk], zero before the first call; plan[4] and
+                                plan[5] count the heads recentred and reset (flag bit 1) so far */
+  float* mu;                 /* [Hk, d] */
+  float* xn; float* mag; float* sq; int32_t* assign;   /* [max_heads, capacity - 1 (, d)] */
+  float* part; int32_t* part_cnt;   /* [max_heads, ceil((capacity - 1) / 256), C (, d)] */
+  int32_t* init_idx;         /* [C_init] */
+  int32_t* mem; int32_t* side; float* proj; float* smag;   /* [capacity]: the division, one head at a time */
+  float* parts;              /* [2, 1024, d] */
+  int32_t* over;             /* [Hk] */
+} ssa_maint_args_t;
+
+/* The recentring and refits the host check between graph replays performs, on the device and
+ * with no host read: heads whose drift flag (bit 0) is set, and not bit 1, are rebuilt around
+ * the mean of their binned keys with their centroids kept (labels, summaries, ksum, rbar, int8
+ * copies); with refit, heads with bit 1 (or every head, with refit_all) are fitted again by
+ * k-means from C_init clusters (seed members as torch.randperm on a CPU generator seeded with
+ * seed), given a cap, and the clusters over it divided as after the prompt fit. Then all flags
+ * are cleared. The state must be one layer's (n_heads == heads_per_layer), all heads with the
+ * same binned length, capacity <= 65536. Every launch reads the flags and lengths from device
+ * memory, so the call can be captured once and replayed every check_every steps.
+ * Replaces SphereIndexFused._check_flags / _act_on / _rebuild (src/ssa/kernels/sphere_fused.py:
+ * 434-464), SphereIndexGPU._reset_heads (src/ssa/attn/sphere_gpu.py:283-293) and
+ * SphereIndexGraph.after_replay / _refit (src/ssa/kernels/graph_kernels.py:260-279), acting on
+ * the flags as the reference's synchronous check (async_check=False) does. */
+int ssa_maintain(const ssa_index_state_t* st, const ssa_maint_args_t* a, void* stream);
+
 /* ---- glue of the captured whole-model decode step -----------------------------------------
  * These have no counterpart in the reference's path: its graph decoder runs the engine's own
  * torch modules between the attention calls (src/ssa/models/graph_decode.py:96-124). Here each

@@ -90,9 +90,36 @@ __global__ __launch_bounds__(kT) void index_kernel(IndexArgs A) {
 struct BuildArgs {
   ssa_index_state_t st;
   ssa_build_args_t b;
-  int nb, nblk;
-  float cap_value;
+  int nb, nblk;        // keys and blocks of the range; with a device plan, the maxima (scratch strides)
+  // Device plan (ssa_maintain): the heads of this pass are b.heads[0, min(*dcount - dcount_off,
+  // b.n_sel)) and the range is [b.start, *dend), both read by the kernels; the grids cover the
+  // maxima and the workgroups past them return at once. The fit's cap, when set_cap, is
+  // cap_keys if > 0 else cap_sf * nb / C_fit (in double, stored as float).
+  const int32_t* dcount; int dcount_off;
+  const int32_t* dend;
+  int set_cap; float cap_keys; double cap_sf;
 };
+
+// The actual head count, range end, key count and block count of a build pass.
+struct BuildDims {
+  int nsel, end, nb, nblk;
+};
+
+__device__ __forceinline__ BuildDims build_dims(const BuildArgs& A) {
+  BuildDims D;
+  if (A.dend) {
+    D.nsel = min(max(*A.dcount - A.dcount_off, 0), A.b.n_sel);
+    D.end = min(*A.dend, A.b.start + A.nb);
+    D.nb = max(D.end - A.b.start, 0);
+    D.nblk = (D.nb + kKB - 1) / kKB;
+  } else {
+    D.nsel = A.b.n_sel;
+    D.end = A.b.end;
+    D.nb = A.nb;
+    D.nblk = A.nblk;
+  }
+  return D;
+}
 
 __device__ __forceinline__ const char* head_keys(const BuildArgs& A, int h) {
   return reinterpret_cast<const char*>(A.b.k) + (int64_t)elem_size(A.b.k_dtype) * (int64_t)h * A.b.s_kh;
@@ -102,10 +129,12 @@ __device__ __forceinline__ const char* head_keys(const BuildArgs& A, int h) {
 // keys, into part[s][b][0][:].
 template <typename T>
 __global__ __launch_bounds__(kT) void center_part_kernel(BuildArgs A, int ncl) {
-  const int s = blockIdx.y, h = A.b.heads[s], b = blockIdx.x, tid = threadIdx.x, d = A.st.d;
-  if (tid >= d) return;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y, b = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  if (tid >= d || s >= Dm.nsel || b >= Dm.nblk) return;
+  const int h = A.b.heads[s];
   KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
-  const int p0 = A.b.start + b * kKB, p1 = min(p0 + kKB, A.b.end);
+  const int p0 = A.b.start + b * kKB, p1 = min(p0 + kKB, Dm.end);
   // loads are issued 32 positions ahead of the adds
   float ks = 0.f;
   int p = p0;
@@ -123,11 +152,14 @@ __global__ __launch_bounds__(kT) void center_part_kernel(BuildArgs A, int ncl) {
 // Centre, stage 2: ksum = left-to-right sum of the block sums, mu = given or ksum / nb; reset the
 // summaries.
 __global__ __launch_bounds__(kT) void center_kernel(BuildArgs A, int ncl) {
-  const int s = blockIdx.x, h = A.b.heads[s], tid = threadIdx.x;
-  const int d = A.st.d, C = A.st.C, nb = A.nb;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.x, tid = threadIdx.x;
+  if (s >= Dm.nsel) return;
+  const int h = A.b.heads[s];
+  const int d = A.st.d, C = A.st.C, nb = Dm.nb;
   if (tid < d) {
     float ks = 0.f;
-    for (int b = 0; b < A.nblk; ++b) ks = ks + A.b.part[(((int64_t)s * A.nblk + b) * ncl) * d + tid];
+    for (int b = 0; b < Dm.nblk; ++b) ks = ks + A.b.part[(((int64_t)s * A.nblk + b) * ncl) * d + tid];
     A.st.ksum[(int64_t)h * d + tid] = ks;
     float mu;
     if (A.b.mu) mu = A.b.mu[(int64_t)s * d + tid];
@@ -142,10 +174,11 @@ __global__ __launch_bounds__(kT) void center_kernel(BuildArgs A, int ncl) {
     A.st.count[(int64_t)h * C + c] = 0;
   }
   if (tid == 0) {
-    A.st.end[h] = A.b.end;
+    A.st.end[h] = Dm.end;
     if (A.b.fit) {
       A.st.n_c[h] = A.b.C_fit;
-      if (A.cap_value > 0.f) A.st.cap[h] = A.cap_value;
+      if (A.set_cap && nb > 0)
+        A.st.cap[h] = A.cap_keys > 0.f ? A.cap_keys : (float)(A.cap_sf * (double)nb / (double)A.b.C_fit);
     }
   }
 }
@@ -157,10 +190,13 @@ template <typename T, int D>
 __global__ __launch_bounds__(kT) void normalize_kernel(BuildArgs A, int ncl) {
   static_assert(kKB == kT, "one block of the squared-length sums per workgroup");
   __shared__ float s_sq[kT];
-  const int s = blockIdx.y, h = A.b.heads[s];
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y;
+  if (s >= Dm.nsel || (int)blockIdx.x >= Dm.nblk) return;   // uniform over the workgroup
+  const int h = A.b.heads[s];
   const int j = blockIdx.x * kT + threadIdx.x;
   float sq = 0.f;
-  if (j < A.nb) {
+  if (j < Dm.nb) {
     KeysT<T> K{reinterpret_cast<const T*>(head_keys(A, h)), A.b.s_kn};
     const float* mu = A.st.mu_ref + (int64_t)h * D;
     const int p = A.b.start + j;
@@ -180,7 +216,7 @@ __global__ __launch_bounds__(kT) void normalize_kernel(BuildArgs A, int ncl) {
   s_sq[threadIdx.x] = sq;
   __syncthreads();                                  // reached by every thread once
   if (threadIdx.x == 0) {
-    const int nk = min(kT, A.nb - blockIdx.x * kT);
+    const int nk = min(kT, Dm.nb - (int)blockIdx.x * kT);
     float t = 0.f;
     for (int u = 0; u < nk; ++u) t = t + s_sq[u];
     A.b.part[(((int64_t)s * A.nblk + blockIdx.x) * ncl + 1) * D] = t;
@@ -189,16 +225,21 @@ __global__ __launch_bounds__(kT) void normalize_kernel(BuildArgs A, int ncl) {
 
 // rbar = sqrt(left-to-right sum of the block sums of squared lengths / nb).
 __global__ void rbar_kernel(BuildArgs A, int ncl) {
-  const int s = blockIdx.x, h = A.b.heads[s];
-  if (threadIdx.x != 0) return;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.x;
+  if (threadIdx.x != 0 || s >= Dm.nsel) return;
+  const int h = A.b.heads[s];
   float t = 0.f;
-  for (int b = 0; b < A.nblk; ++b) t = t + A.b.part[(((int64_t)s * A.nblk + b) * ncl + 1) * A.st.d];
-  A.st.rbar[h] = A.nb > 0 ? sqrtf(t / (float)A.nb) : 0.f;
+  for (int b = 0; b < Dm.nblk; ++b) t = t + A.b.part[(((int64_t)s * A.nblk + b) * ncl + 1) * A.st.d];
+  A.st.rbar[h] = Dm.nb > 0 ? sqrtf(t / (float)Dm.nb) : 0.f;
 }
 
 // k-means seed: centroid c is the unit direction of range member init_idx[c].
 __global__ __launch_bounds__(kT) void kmeans_init_kernel(BuildArgs A) {
-  const int s = blockIdx.y, h = A.b.heads[s], c = blockIdx.x, d = A.st.d;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y, c = blockIdx.x, d = A.st.d;
+  if (s >= Dm.nsel || Dm.nb <= 0) return;
+  const int h = A.b.heads[s];
   const int j = A.b.init_idx[c];
   if (threadIdx.x < d)
     A.st.cent[((int64_t)h * A.st.C + c) * d + threadIdx.x] = A.b.xn[((int64_t)s * A.nb + j) * d + threadIdx.x];
@@ -270,7 +311,11 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
   __shared__ int lst[kW][LIST];                      // candidates: key << 16 | centroid
   __shared__ unsigned long long rk[kW][NK];              // best (score desc, index asc) per key
   __shared__ int kcnt[kW][NK], kfirst[kW][NK];
-  const int s = blockIdx.y, h = A.b.heads[s], tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (s >= Dm.nsel || (int)blockIdx.x * asg_keys<D>() >= Dm.nb) return;   // uniform over the workgroup
+  const int h = A.b.heads[s];
+  const int nb = Dm.nb;
   const int nc = A.st.n_c[h];
   const float* cent = A.st.shared_dirs ? A.st.cent : A.st.cent + (int64_t)h * A.st.C * D;
   const float* xn = A.b.xn + (int64_t)s * A.nb * D;
@@ -280,7 +325,7 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
   bf16x8 af[KG][KS];
 #pragma unroll
   for (int g = 0; g < KG; ++g) {
-    const float* xa = xn + (int64_t)min(j0 + 16 * g + r16, A.nb - 1) * D;
+    const float* xa = xn + (int64_t)min(j0 + 16 * g + r16, nb - 1) * D;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) af[g][ks] = frag8<D>(xa, 32 * ks + 8 * g4);
   }
@@ -379,7 +424,7 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kl = 16 * g + 4 * g4 + i;
-          const bool cand = c < nc && j0 + kl < A.nb && acc[g][i] >= thr[g][i];
+          const bool cand = c < nc && j0 + kl < nb && acc[g][i] >= thr[g][i];
           cnt[g][i] += cand ? 1 : 0;
           first[g][i] = cand ? min(first[g][i], c) : first[g][i];
           const unsigned long long m = __ballot(cand);
@@ -402,7 +447,7 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
   __syncthreads();
   if (lane < NK) {
     const int j = j0 + lane;
-    if (j < A.nb) {
+    if (j < nb) {
       const int k = kcnt[wave][lane];
       // no candidate: every score of the key is NaN (a non-finite key); it joins cluster 0, the
       // first index, as torch.argmax picks on a row of NaNs
@@ -418,8 +463,11 @@ __global__ __launch_bounds__(kT) void assign_kernel(BuildArgs A, int write_label
 // also fold the members' lengths into mmax / mmin (order-free max / min).
 __global__ __launch_bounds__(kT) void block_sum_kernel(BuildArgs A, int ncl, int summaries) {
   __shared__ int s_as[kKB], s_order[kKB], s_start[kMaxC + 1], s_cnt[kMaxC];
-  const int s = blockIdx.y, h = A.b.heads[s], b = blockIdx.x, tid = threadIdx.x, d = A.st.d;
-  const int j0 = b * kKB, nk = min(kKB, A.nb - j0);
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y, b = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  if (s >= Dm.nsel || b >= Dm.nblk) return;   // uniform over the workgroup
+  const int h = A.b.heads[s];
+  const int j0 = b * kKB, nk = min(kKB, Dm.nb - j0);
   const int* as = A.b.assign + (int64_t)s * A.nb + j0;
   for (int c = tid; c < ncl; c += kT) s_cnt[c] = 0;
   __syncthreads();
@@ -468,7 +516,11 @@ __global__ __launch_bounds__(kT) void block_reduce_kernel(BuildArgs A, int ncl, 
   __shared__ float v[kMaxD];
   __shared__ float s_r;
   __shared__ int s_n;
-  const int s = blockIdx.y, h = A.b.heads[s], c = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  if (s >= Dm.nsel) return;                         // uniform over the workgroup
+  const int h = A.b.heads[s];
+  const int nblk = Dm.nblk;
   if (tid == 0) s_n = 0;
   __syncthreads();
   if (tid < d) {
@@ -477,18 +529,18 @@ __global__ __launch_bounds__(kT) void block_reduce_kernel(BuildArgs A, int ncl, 
     const int64_t st = (int64_t)ncl * d;
     float acc = 0.f;
     int b = 0;
-    for (; b + 16 <= A.nblk; b += 16) {
+    for (; b + 16 <= nblk; b += 16) {
       float x[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) x[u] = pp[(b + u) * st];
 #pragma unroll
       for (int u = 0; u < 16; ++u) acc = acc + x[u];
     }
-    for (; b < A.nblk; ++b) acc = acc + pp[b * st];
+    for (; b < nblk; ++b) acc = acc + pp[b * st];
     v[tid] = acc;
   }
   int n = 0;                                        // integer counts: any order
-  for (int b = tid; b < A.nblk; b += kT) n += A.b.part_cnt[((int64_t)s * A.nblk + b) * ncl + c];
+  for (int b = tid; b < nblk; b += kT) n += A.b.part_cnt[((int64_t)s * A.nblk + b) * ncl + c];
   if (n) atomicAdd(&s_n, n);
   __syncthreads();
   const int64_t row = ((int64_t)h * A.st.C + c) * d;
@@ -507,7 +559,10 @@ __global__ __launch_bounds__(kT) void block_reduce_kernel(BuildArgs A, int ncl, 
 __global__ __launch_bounds__(kT) void refresh8_kernel(BuildArgs A) {
   __shared__ float v[kMaxD];
   __shared__ float s_r;
-  const int s = blockIdx.y, h = A.b.heads[s], c = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  const BuildDims Dm = build_dims(A);
+  const int s = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, d = A.st.d;
+  if (s >= Dm.nsel) return;                         // uniform over the workgroup
+  const int h = A.b.heads[s];
   const int64_t row = ((int64_t)h * A.st.C + c) * d;
   for (int pass = 0; pass < 2; ++pass) {
     const float* src = pass == 0 ? A.st.sum_dir : A.st.cent;
@@ -648,17 +703,22 @@ __device__ __forceinline__ void fit_kmeans(FitSmem& S, const PartRows& P, const 
   }
 }
 
+// The range, cap floor, round kind and scratch slot of one head's division.
+struct FitCtx {
+  int start, end;
+  float cap_min;
+  int nmeans;
+  int slot;       // row of a.mem / side / proj / smag and of a.parts used for this head
+};
+
+// One round of the division for head a.heads[s], whose first cluster over the cap has global
+// rank r0 in the round. Returns the clusters divided, or -1 when a division found no room.
 template <int D>
-__global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
-  __shared__ FitSmem S;
+__device__ __forceinline__ int fit_split_head(FitSmem& S, const FitArgs& A, int s, int r0, const FitCtx& X) {
   const ssa_index_state_t& st = A.st;
   const ssa_split_args_t& a = A.a;
-  const int s = blockIdx.x, h = a.heads[s], tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, C = st.C;
-  const float cap = fit_cap(A, h);
-  // global rank of this head's first cluster over the cap: heads are taken in order
-  int r0 = 0;
-  for (int t = tid; t < s; t += kT) r0 += a.over[t];
-  r0 = block_sum_i(S, r0);
+  const int h = a.heads[s], tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, C = st.C;
+  const float cap = fmaxf(st.cap[h], X.cap_min);
   const int n_act0 = min(st.n_c[h], C);
   if (tid == 0) { S.nlist = 0; S.bad = 0; }
   __syncthreads();
@@ -676,10 +736,10 @@ __global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
     __syncthreads();
   }
   Head H = head_view(st, h);
-  H.mem = a.mem + (int64_t)s * a.ms;
-  H.side = a.side + (int64_t)s * a.ms;
-  H.proj = a.proj + (int64_t)s * a.ms;
-  H.smag = a.smag + (int64_t)s * a.ms;
+  H.mem = a.mem + (int64_t)X.slot * a.ms;
+  H.side = a.side + (int64_t)X.slot * a.ms;
+  H.proj = a.proj + (int64_t)X.slot * a.ms;
+  H.smag = a.smag + (int64_t)X.slot * a.ms;
   H.ms = a.ms;
   Keys K;
   K.dt = a.k_dtype;
@@ -692,15 +752,15 @@ __global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
   for (int i = 0; i < nlist; ++i) {
     const int c = S.list[i];
     if ((r0 + i) % 64 == 0) base = n_cur;                 // a new batch of 64
-    if (!a.nmeans) {
+    if (!X.nmeans) {
       if (base + 1 <= C) {
-        split_cluster(S, st, H, K, h, c, base, a.end);
+        split_cluster(S, st, H, K, h, c, base, X.end);
         if (st.n_c[h] == base + 1) { n_cur = base + 1; ++done; }
       }
       base += 1;
       continue;
     }
-    const int m = gather_members(S, H, c, a.start, a.end);
+    const int m = gather_members(S, H, c, X.start, X.end);
     for (int j = tid; j < m; j += kT) {
       const int pos = H.mem[j];
       auto kr = [&](int t) { return K(pos, t) - S.mu[t]; };
@@ -717,7 +777,7 @@ __global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
         __syncthreads();
         continue;
       }
-      float* base_p = a.parts + (int64_t)s * 2 * a.max_parts * D;
+      float* base_p = a.parts + (int64_t)X.slot * 2 * a.max_parts * D;
       P = PartRows{base_p, base_p + (int64_t)a.max_parts * D, D};
     }
     fit_kmeans(S, P, H, K, m, k, a.iters);
@@ -760,7 +820,183 @@ __global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
     base += extra > 0 ? extra : 0;
     __syncthreads();
   }
-  if (tid == 0) a.done[s] = S.bad ? -1 : done;
+  const int bad = S.bad;
+  __syncthreads();                                     // S is reused by the caller
+  return bad ? -1 : done;
+}
+
+template <int D>
+__global__ __launch_bounds__(kT) void fit_split_kernel(FitArgs A) {
+  __shared__ FitSmem S;
+  const int s = blockIdx.x;
+  // global rank of this head's first cluster over the cap: heads are taken in order
+  int r0 = 0;
+  for (int t = threadIdx.x; t < s; t += kT) r0 += A.a.over[t];
+  r0 = block_sum_i(S, r0);
+  const int done = fit_split_head<D>(S, A, s, r0, FitCtx{A.a.start, A.a.end, A.a.cap_min, A.a.nmeans, s});
+  if (threadIdx.x == 0) A.a.done[s] = done;
+}
+
+// ---- maintenance on the device (ssa_maintain) -------------------------------------------------
+//
+// Reference: SphereIndexFused._check_flags / _act_on / _rebuild (src/ssa/kernels/sphere_fused.py:
+// 434-464), SphereIndexGPU._reset_heads (src/ssa/attn/sphere_gpu.py:283-293) and
+// SphereIndexGraph._refit (src/ssa/kernels/graph_kernels.py:270-279), acting on the flags at the
+// check as the reference's synchronous check does. The plan kernel decides on the device which
+// heads are rebuilt; every later launch reads that plan, so the sequence can be captured once.
+//
+// Plan words: [0] heads to recentre, [1] heads to refit, [2] binned end, [3] 1 if a division
+// found no room for its parts, [4] heads recentred so far, [5] heads reset so far, [6] rounds
+// of the last division, [7] heads whose int8 copies the division refreshes (all, or 0); then
+// SSA_MAINT_PLAN_WORDS + [0, n): heads to recentre, + [n, 2n): heads to refit, + [2n, 3n): all.
+
+struct MaintArgs {
+  ssa_maint_args_t m;
+  int n;                      // heads of the layer
+};
+
+__global__ __launch_bounds__(kT) void maint_plan_kernel(ssa_index_state_t st, MaintArgs M) {
+  __shared__ int s_nrec;
+  const int n = M.n, d = st.d, tid = threadIdx.x;
+  int32_t* plan = M.m.plan;
+  int32_t* rec = plan + SSA_MAINT_PLAN_WORDS;
+  int32_t* ref = rec + n;
+  int32_t* all = ref + n;
+  const int end = st.end[0];
+  const int nb = end - 1;
+  if (tid == 0) {
+    int a = 0, b = 0;
+    for (int h = 0; h < n; ++h) {
+      const int f = st.flags[h];
+      if (M.m.refit && (M.m.refit_all || (f & 2))) ref[b++] = h;        // refit (bit 1 wins over bit 0)
+      else if (!M.m.refit_all && !(f & 2) && (f & 1) && nb > 0) rec[a++] = h;
+    }
+    s_nrec = a;
+    plan[0] = a;
+    plan[1] = b;
+    plan[2] = end;
+    plan[3] = 0;
+    plan[4] += a;
+    if (!M.m.refit_all) plan[5] += b;                  // resets; refits of every head are counted by the host
+    plan[7] = (b > 0 && M.m.split_factor > 0.f) ? n : 0;
+  }
+  for (int h = tid; h < n; h += kT) all[h] = h;
+  __syncthreads();
+  // the centring mean of a recentred head: its running key sum over the binned keys
+  for (int e = tid; e < s_nrec * d; e += kT) {
+    const int i = e / d, t = e % d;
+    M.m.mu[(int64_t)i * d + t] = st.ksum[(int64_t)rec[i] * d + t] / (float)nb;
+  }
+  for (int h = tid; h < n; h += kT) st.flags[h] = 0;   // thread 0 read them before the barrier
+}
+
+// Seed members of a refit: init_idx[c] = torch.randperm(nb, generator seeded with seed)[c % nb]
+// for c < C_init (src/ssa/attn/clusterkv.py:34-36). torch's CPU randperm is a Fisher-Yates
+// shuffle driven by MT19937 seeded by init_genrand: step i swaps r[i] with r[i + (draw % (nb -
+// i))], a draw being the next 32-bit tempered output. r[0, C) is final after C steps, and only
+// the swapped positions are stored (a hash map in LDS; identity elsewhere). One thread; refits are
+// rare.
+constexpr int kPermMap = 4096;          // > 2 * 1024 swapped positions
+
+__global__ __launch_bounds__(64) void maint_randperm_kernel(MaintArgs M) {
+  __shared__ uint32_t mt[624];
+  __shared__ int key[kPermMap], val[kPermMap];
+  const int32_t* plan = M.m.plan;
+  if (plan[1] == 0) return;
+  const int nb = plan[2] - 1;
+  if (nb <= 0) return;
+  for (int i = threadIdx.x; i < kPermMap; i += 64) key[i] = -1;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  uint32_t x = (uint32_t)M.m.seed;
+  mt[0] = x;
+  for (int k = 1; k < 624; ++k) {
+    x = 1812433253u * (x ^ (x >> 30)) + (uint32_t)k;
+    mt[k] = x;
+  }
+  int mi = 624;
+  auto draw = [&]() -> uint32_t {
+    if (mi >= 624) {
+      for (int k = 0; k < 624; ++k) {
+        const uint32_t y = (mt[k] & 0x80000000u) | (mt[k + 1 < 624 ? k + 1 : 0] & 0x7fffffffu);
+        mt[k] = mt[k + 397 < 624 ? k + 397 : k + 397 - 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+      }
+      mi = 0;
+    }
+    uint32_t y = mt[mi++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+  };
+  auto slot = [&](int pos) {
+    unsigned h = ((unsigned)pos * 2654435761u) >> 20;
+    while (key[h] != -1 && key[h] != pos) h = (h + 1) & (kPermMap - 1);
+    return h;
+  };
+  auto get = [&](int pos) {
+    const unsigned h = slot(pos);
+    return key[h] == pos ? val[h] : pos;
+  };
+  auto put = [&](int pos, int v) {
+    const unsigned h = slot(pos);
+    key[h] = pos;
+    val[h] = v;
+  };
+  const int C = M.m.C_init;
+  const int steps = min(C, nb - 1);
+  for (int i = 0; i < steps; ++i) {
+    const int j = i + (int)(draw() % (uint32_t)(nb - i));
+    const int vi = get(i), vj = get(j);
+    put(i, vj);
+    put(j, vi);
+  }
+  for (int c = 0; c < C; ++c) M.m.init_idx[c] = get(c % nb);
+}
+
+// The division after a refit: one workgroup runs the rounds of the host loop of
+// SphereIndexFused._split_overflow (a k-means round, then bisection rounds, until no cluster is
+// over its cap or a bisection round divides nothing) over every head of the layer, heads in order
+// within a round (the global ranks of ssa_split_fit), one head's member scratch at a time.
+template <int D>
+__global__ __launch_bounds__(kT) void maint_divide_kernel(FitArgs A, MaintArgs M) {
+  __shared__ FitSmem S;
+  int32_t* plan = M.m.plan;
+  if (plan[7] == 0) return;
+  const int end = plan[2], start = 1, n = M.n;
+  const float cap_min = (float)(M.m.capk * (double)(end - start));
+  int nmeans = 1, rounds = 0;
+  for (;;) {
+    int over_tot = 0;
+    for (int s2 = 0; s2 < n; ++s2) {
+      const int h = A.a.heads[s2];
+      const float cap = fmaxf(A.st.cap[h], cap_min);
+      const int n_act = min(A.st.n_c[h], A.st.C);
+      int c0 = 0;
+      for (int c = threadIdx.x; c < n_act; c += kT) c0 += fit_over(A, h, c, cap) ? 1 : 0;
+      c0 = block_sum_i(S, c0);
+      if (threadIdx.x == 0) A.a.over[s2] = c0;
+      over_tot += c0;
+    }
+    __syncthreads();                                   // A.a.over written
+    int r0 = 0, done_tot = 0;
+    bool bad = false;
+    for (int s2 = 0; s2 < n && !bad; ++s2) {
+      const int dn = fit_split_head<D>(S, A, s2, r0, FitCtx{start, end, cap_min, nmeans, 0});
+      r0 += A.a.over[s2];
+      if (dn < 0) bad = true;
+      else done_tot += dn;
+    }
+    ++rounds;
+    if (bad) {
+      if (threadIdx.x == 0) plan[3] = 1;
+      break;
+    }
+    if (over_tot == 0 || (done_tot == 0 && !nmeans)) break;
+    nmeans = 0;
+  }
+  if (threadIdx.x == 0) plan[6] = rounds;
 }
 
 }  // namespace ssa
@@ -853,29 +1089,27 @@ extern "C" int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* 
   return launch_index(A, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b, void* stream) {
-  if (!state_ok(st) || !b || b->n_sel < 1 || b->start < 0 || b->end < b->start || b->end > st->capacity)
-    return hipErrorInvalidValue;
-  if (b->fit && (b->C_fit < 1 || b->C_fit > st->C || b->C_fit > kKB * 4 || !b->init_idx)) return hipErrorInvalidValue;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  BuildArgs A{};
-  A.st = *st;
-  A.b = *b;
-  A.nb = b->end - b->start;
-  A.nblk = (A.nb + kKB - 1) / kKB;
-  A.cap_value = 0.f;
+namespace {
+
+// The kernels of a build pass over A's heads (centre, optionally fit, bin, summarise, and the
+// int8 copies when refresh). With a device plan (A.dend) every kernel is launched for the
+// maxima and reads the actual heads and range itself.
+void launch_build(const BuildArgs& A, int fit, bool refresh, hipStream_t s) {
+  const ssa_index_state_t* st = &A.st;
+  const int n_sel = A.b.n_sel;
   const int ncl = st->C;                           // part[] holds at least C slots per block
-  if (A.nb > 0) {
-    const dim3 gb(A.nblk, b->n_sel);
-    switch (b->k_dtype) {
+  const bool dev = A.dend != nullptr;
+  if (dev || A.nb > 0) {
+    const dim3 gb(A.nblk, n_sel);
+    switch (A.b.k_dtype) {
       case kBF16: hipLaunchKernelGGL(center_part_kernel<__hip_bfloat16>, gb, dim3(kT), 0, s, A, ncl); break;
       case kF16: hipLaunchKernelGGL(center_part_kernel<__half>, gb, dim3(kT), 0, s, A, ncl); break;
       default: hipLaunchKernelGGL(center_part_kernel<float>, gb, dim3(kT), 0, s, A, ncl); break;
     }
   }
-  hipLaunchKernelGGL(center_kernel, dim3(b->n_sel), dim3(kT), 0, s, A, ncl);
-  if (A.nb > 0) {
-    dim3 gk((A.nb + kT - 1) / kT, b->n_sel);
+  hipLaunchKernelGGL(center_kernel, dim3(n_sel), dim3(kT), 0, s, A, ncl);
+  if (dev || A.nb > 0) {
+    dim3 gk((A.nb + kT - 1) / kT, n_sel);
     auto normalize = [&](auto tag) {
       using T = decltype(tag);
       switch (st->d) {
@@ -886,13 +1120,13 @@ extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b,
         case 256: hipLaunchKernelGGL((normalize_kernel<T, 256>), gk, dim3(kT), 0, s, A, ncl); break;
       }
     };
-    if (b->k_dtype == kBF16) normalize(__hip_bfloat16{});
-    else if (b->k_dtype == kF16) normalize(__half{});
+    if (A.b.k_dtype == kBF16) normalize(__hip_bfloat16{});
+    else if (A.b.k_dtype == kF16) normalize(__half{});
     else normalize(0.f);
-    hipLaunchKernelGGL(rbar_kernel, dim3(b->n_sel), dim3(64), 0, s, A, ncl);
+    hipLaunchKernelGGL(rbar_kernel, dim3(n_sel), dim3(64), 0, s, A, ncl);
     auto assign = [&](int write_labels) {
       auto go = [&](auto kern, int keys) {
-        hipLaunchKernelGGL(kern, dim3((A.nb + keys - 1) / keys, b->n_sel), dim3(kT), 0, s, A, write_labels);
+        hipLaunchKernelGGL(kern, dim3((A.nb + keys - 1) / keys, n_sel), dim3(kT), 0, s, A, write_labels);
       };
       switch (st->d) {
         case 16: go(assign_kernel<16>, asg_keys<16>()); break;
@@ -902,18 +1136,125 @@ extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b,
         case 256: go(assign_kernel<256>, asg_keys<256>()); break;
       }
     };
-    if (b->fit && !st->shared_dirs) {
-      hipLaunchKernelGGL(kmeans_init_kernel, dim3(b->C_fit, b->n_sel), dim3(kT), 0, s, A);
-      for (int it = 0; it < b->iters; ++it) {
+    if (fit && !st->shared_dirs) {
+      hipLaunchKernelGGL(kmeans_init_kernel, dim3(A.b.C_fit, n_sel), dim3(kT), 0, s, A);
+      for (int it = 0; it < A.b.iters; ++it) {
         assign(0);
-        hipLaunchKernelGGL(block_sum_kernel, dim3(A.nblk, b->n_sel), dim3(kT), 0, s, A, b->C_fit, 0);
-        hipLaunchKernelGGL(block_reduce_kernel, dim3(b->C_fit, b->n_sel), dim3(kT), 0, s, A, b->C_fit, 0);
+        hipLaunchKernelGGL(block_sum_kernel, dim3(A.nblk, n_sel), dim3(kT), 0, s, A, A.b.C_fit, 0);
+        hipLaunchKernelGGL(block_reduce_kernel, dim3(A.b.C_fit, n_sel), dim3(kT), 0, s, A, A.b.C_fit, 0);
       }
     }
     assign(1);
-    hipLaunchKernelGGL(block_sum_kernel, dim3(A.nblk, b->n_sel), dim3(kT), 0, s, A, st->C, 1);
-    hipLaunchKernelGGL(block_reduce_kernel, dim3(st->C, b->n_sel), dim3(kT), 0, s, A, st->C, 1);
+    hipLaunchKernelGGL(block_sum_kernel, dim3(A.nblk, n_sel), dim3(kT), 0, s, A, st->C, 1);
+    hipLaunchKernelGGL(block_reduce_kernel, dim3(st->C, n_sel), dim3(kT), 0, s, A, st->C, 1);
   }
-  if (st->dir8 || st->cent8) hipLaunchKernelGGL(refresh8_kernel, dim3(st->C, b->n_sel), dim3(kT), 0, s, A);
+  if (refresh && (st->dir8 || st->cent8)) hipLaunchKernelGGL(refresh8_kernel, dim3(st->C, n_sel), dim3(kT), 0, s, A);
+}
+
+template <int D>
+void launch_divide(const FitArgs& F, const MaintArgs& M, hipStream_t s) {
+  hipLaunchKernelGGL(maint_divide_kernel<D>, dim3(1), dim3(kT), 0, s, F, M);
+}
+
+}  // namespace
+
+extern "C" int ssa_build(const ssa_index_state_t* st, const ssa_build_args_t* b, void* stream) {
+  if (!state_ok(st) || !b || b->n_sel < 1 || b->start < 0 || b->end < b->start || b->end > st->capacity)
+    return hipErrorInvalidValue;
+  if (b->fit && (b->C_fit < 1 || b->C_fit > st->C || b->C_fit > kKB * 4 || !b->init_idx)) return hipErrorInvalidValue;
+  BuildArgs A{};
+  A.st = *st;
+  A.b = *b;
+  A.nb = b->end - b->start;
+  A.nblk = (A.nb + kKB - 1) / kKB;
+  launch_build(A, b->fit, true, reinterpret_cast<hipStream_t>(stream));
+  return hipGetLastError();
+}
+
+extern "C" int ssa_maintain(const ssa_index_state_t* st, const ssa_maint_args_t* a, void* stream) {
+  if (!state_ok(st) || !a || st->n_heads != st->heads_per_layer || st->capacity > 65536 || st->capacity < 2 ||
+      !a->k || !a->plan || !a->mu || !a->xn || !a->mag || !a->sq || !a->assign || !a->part || !a->part_cnt ||
+      a->max_heads < 1)
+    return hipErrorInvalidValue;
+  if (a->refit && (st->shared_dirs || a->C_init < 1 || a->C_init > st->C || a->C_init > kKB * 4 || a->iters < 0 ||
+                   !a->init_idx || !a->mem || !a->side || !a->proj || !a->smag || !a->parts || !a->over))
+    return hipErrorInvalidValue;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int n = st->n_heads, P = min(a->max_heads, n), passes = (n + P - 1) / P;
+  MaintArgs M{};
+  M.m = *a;
+  M.n = n;
+  hipLaunchKernelGGL(maint_plan_kernel, dim3(1), dim3(kT), 0, s, *st, M);
+  int32_t* rec = a->plan + SSA_MAINT_PLAN_WORDS;
+  int32_t* ref = rec + n;
+  int32_t* all = ref + n;
+  BuildArgs B{};
+  B.st = *st;
+  B.b.k = a->k; B.b.k_dtype = a->k_dtype; B.b.s_kh = a->s_kh; B.b.s_kn = a->s_kn;
+  B.b.start = 1;
+  B.b.end = st->capacity;
+  B.b.xn = a->xn; B.b.mag = a->mag; B.b.sq = a->sq; B.b.assign = a->assign;
+  B.b.part = a->part; B.b.part_cnt = a->part_cnt;
+  B.nb = st->capacity - 1;                           // scratch strides: the largest binned range
+  B.nblk = (B.nb + kKB - 1) / kKB;
+  B.dend = a->plan + 2;
+  if (a->refit) {
+    hipLaunchKernelGGL(maint_randperm_kernel, dim3(1), dim3(64), 0, s, M);
+    B.b.fit = 1;
+    B.b.C_fit = a->C_init;
+    B.b.iters = a->iters;
+    B.b.init_idx = a->init_idx;
+    B.b.mu = nullptr;
+    B.set_cap = a->split_factor > 0.f;
+    B.cap_keys = a->cap_keys;
+    B.cap_sf = (double)a->split_factor;
+    B.dcount = a->plan + 1;
+    const bool divide = a->split_factor > 0.f;
+    for (int p = 0; p < passes; ++p) {
+      B.b.heads = ref + p * P;
+      B.b.n_sel = P;
+      B.dcount_off = p * P;
+      launch_build(B, 1, !divide, s);
+    }
+    if (divide) {
+      FitArgs F{};
+      F.st = *st;
+      F.a.k = a->k; F.a.k_dtype = a->k_dtype; F.a.s_kh = a->s_kh; F.a.s_kn = a->s_kn;
+      F.a.heads = all; F.a.n_sel = n;
+      F.a.start = 1;
+      F.a.split_factor = a->split_factor;
+      F.a.iters = a->iters;
+      F.a.mem = a->mem; F.a.side = a->side; F.a.proj = a->proj; F.a.smag = a->smag;
+      F.a.ms = st->capacity;
+      F.a.over = a->over;
+      F.a.parts = a->parts;
+      F.a.max_parts = kMaxParts;
+      switch (st->d) {
+        case 16: launch_divide<16>(F, M, s); break;
+        case 32: launch_divide<32>(F, M, s); break;
+        case 64: launch_divide<64>(F, M, s); break;
+        case 128: launch_divide<128>(F, M, s); break;
+        case 256: launch_divide<256>(F, M, s); break;
+      }
+      // the int8 copies of every head after the division (plan[7] is n when a head was refitted)
+      BuildArgs R = B;
+      R.b.heads = all;
+      R.b.n_sel = n;
+      R.dcount = a->plan + 7;
+      R.dcount_off = 0;
+      if (st->dir8 || st->cent8) hipLaunchKernelGGL(refresh8_kernel, dim3(st->C, n), dim3(kT), 0, s, R);
+    }
+  }
+  // recentre: the flagged heads' centroids are kept (no fit), their mean is ksum / nb
+  B.b.fit = 0;
+  B.set_cap = 0;
+  B.dcount = a->plan + 0;
+  for (int p = 0; p < passes; ++p) {
+    B.b.heads = rec + p * P;
+    B.b.n_sel = P;
+    B.dcount_off = p * P;
+    B.b.mu = a->mu + (int64_t)p * P * st->d;
+    launch_build(B, 0, true, s);
+  }
   return hipGetLastError();
 }

@@ -95,6 +95,25 @@ class SplitArgs(ct.Structure):
                 ("parts", vp), ("max_parts", i32)]
 
 
+class MaintArgs(ct.Structure):
+    _fields_ = [("k", vp), ("k_dtype", i32), ("s_kh", i64), ("s_kn", i64),
+                ("refit_all", i32), ("refit", i32),
+                ("C_init", i32), ("iters", i32), ("seed", i32),
+                ("split_factor", f32), ("cap_keys", f32),
+                ("capk", f64),
+                ("max_heads", i32),
+                ("plan", vp), ("mu", vp),
+                ("xn", vp), ("mag", vp), ("sq", vp), ("assign", vp),
+                ("part", vp), ("part_cnt", vp),
+                ("init_idx", vp),
+                ("mem", vp), ("side", vp), ("proj", vp), ("smag", vp),
+                ("parts", vp),
+                ("over", vp)]
+
+
+MAINT_PLAN_WORDS = 8      # SSA_MAINT_PLAN_WORDS
+
+
 # (name, restype, argtypes) of every exported entry point; the C-ABI test checks this list
 # against the header.
 ENTRY_POINTS = {
@@ -109,6 +128,7 @@ ENTRY_POINTS = {
     "ssa_select": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(InsertArgs), ct.POINTER(SelectArgs), vp]),
     "ssa_build": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(BuildArgs), vp]),
     "ssa_split_fit": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SplitArgs), vp]),
+    "ssa_maintain": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(MaintArgs), vp]),
     "ssa_sparse_step": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs),
                                    ct.POINTER(InsertArgs), vp]),
     "ssa_sparse_step_noalloc": (ct.c_int, [ct.POINTER(IndexState), ct.POINTER(SelectArgs), ct.POINTER(AttnArgs),

@@ -21,9 +21,38 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import check, lib, stream_ptr
+from ._lib import MAINT_PLAN_WORDS, MaintArgs, check, dtype_tag, lib, stream_ptr
 from .labeled_attn import SplitWork, attn_args, cu_count, default_splits
 from .sphere_fused import SphereIndexFused
+
+MAINT_BUDGET = 1 << 30        # bytes of build scratch one maintenance pass may use (shared by all layers)
+
+
+class _MaintScratch:
+    """Scratch of ``ssa_maintain`` for one shape. The layers of a model run their maintenance one
+    after another on one stream, so they share one of these."""
+
+    def __init__(self, n, capacity, C, C_init, d, device):
+        nbmax = capacity - 1
+        nblk = -(-nbmax // 256)
+        per_head = 4 * nbmax * (d + 3) + 4 * nblk * C * (d + 1)
+        self.P = max(1, min(n, MAINT_BUDGET // per_head))
+        P = self.P
+        f32, i32 = dict(dtype=torch.float32, device=device), dict(dtype=torch.int32, device=device)
+        self.mu = torch.empty(n, d, **f32)
+        self.xn = torch.empty(P, nbmax, d, **f32)
+        self.mag, self.sq = torch.empty(P, nbmax, **f32), torch.empty(P, nbmax, **f32)
+        self.assign = torch.empty(P, nbmax, **i32)
+        self.part = torch.empty(P, nblk, C, d, **f32)
+        self.part_cnt = torch.empty(P, nblk, C, **i32)
+        self.init_idx = torch.empty(max(C_init, 1), **i32)
+        self.mem, self.side = torch.empty(capacity, **i32), torch.empty(capacity, **i32)
+        self.proj, self.smag = torch.empty(capacity, **f32), torch.empty(capacity, **f32)
+        self.parts = torch.empty(2, 1024, d, **f32)
+        self.over = torch.empty(n, **i32)
+
+
+_MAINT: dict = {}
 
 STACKED = ("n_c", "sum_dir", "dir8", "cent", "cent8", "mmax", "mmin", "count", "ksum", "mu_ref", "rbar", "flags",
            "cap", "vthr", "_mem", "_proj", "_side", "_smag", "_stage", "nsplit", "labels", "end_dev")
@@ -49,8 +78,14 @@ class SphereIndexGraph(SphereIndexFused):
     """``SphereIndexFused`` for graph capture: ``step`` issues only fixed-argument kernels."""
 
     def __init__(self, *, budget: float, block_n: int = 32, compact_block: int = 1024, refit_every: int = 0,
-                 num_splits: int | None = None, insert_ahead: bool | None = None, **kw):
+                 num_splits: int | None = None, insert_ahead: bool | None = None,
+                 device_maintenance: bool = True, **kw):
+        self._plan = None
         super().__init__(**kw)
+        # recentring, resets and refits on the device (ssa_maintain), with no host read between
+        # replays; the host path (the reference's eager rebuilds) serves var_factor > 0, whose
+        # threshold the device does not recompute
+        self.device_maintenance = device_maintenance and self.var_factor == 0
         self.insert_ahead = insert_ahead          # None: decided at prepare (auto_insert_ahead)
         self.refit_every = refit_every
         self.refits = 0
@@ -114,14 +149,65 @@ class SphereIndexGraph(SphereIndexFused):
         self.end = int(self.end_dev[0])                          # host sync, only when a flag was set
 
     def after_replay(self, K: torch.Tensor) -> None:
-        """Between replays: every ``check_every`` steps read the drift flags without a sync; once
-        a copy has landed, recentre the flagged heads (eager, in place)."""
+        """Between replays: every ``check_every`` steps act on the drift and reset flags, and every
+        ``refit_every`` steps refit every head. With ``device_maintenance`` that is one
+        ``ssa_maintain`` call, which reads the flags on the device (no host read); otherwise the
+        flags are copied without a sync and, once a copy has landed, the flagged heads are
+        rebuilt eagerly, as in the reference."""
         self.head_steps += self.H_kv
         self._steps += 1
-        if self.refit_every and self._steps % self.refit_every == 0:
+        refit = bool(self.refit_every) and self._steps % self.refit_every == 0
+        if self.device_maintenance:
+            if refit or self._steps % self.check_every == 0:
+                self.maintain(K, refit_all=refit)
+            return
+        if refit:
             self._refit(K)
         elif self._steps % self.check_every == 0:
             self._check_flags(K)
+
+    def maintain(self, K: torch.Tensor, *, refit_all: bool = False) -> None:
+        """``ssa_maintain``: recentre the heads whose drift flag is set, refit those whose reset
+        flag is set (or every head, with ``refit_all``), clear the flags; all on the device."""
+        key = (str(self.device), self.H_kv, self.capacity, self.C, self.C_init, self.d)
+        sc = _MAINT.get(key)
+        if sc is None:
+            sc = _MAINT[key] = _MaintScratch(self.H_kv, self.capacity, self.C, self.C_init, self.d, self.device)
+        if self._plan is None:
+            self._plan = torch.zeros(MAINT_PLAN_WORDS + 3 * self.H_kv, dtype=torch.int32, device=self.device)
+        a = MaintArgs()
+        a.k, a.k_dtype, a.s_kh, a.s_kn = K.data_ptr(), dtype_tag(K.dtype), K.stride(0), K.stride(1)
+        a.refit_all = int(refit_all)
+        a.refit = int(refit_all or bool(self.reset_at))
+        a.C_init, a.iters, a.seed = self.C_init, self.kmeans_iters, self.seed
+        a.split_factor, a.cap_keys, a.capk = self.split_factor, self.cap_keys, self.capk
+        a.max_heads = sc.P
+        a.plan, a.mu = self._plan.data_ptr(), sc.mu.data_ptr()
+        a.xn, a.mag, a.sq, a.assign = sc.xn.data_ptr(), sc.mag.data_ptr(), sc.sq.data_ptr(), sc.assign.data_ptr()
+        a.part, a.part_cnt, a.init_idx = sc.part.data_ptr(), sc.part_cnt.data_ptr(), sc.init_idx.data_ptr()
+        a.mem, a.side, a.proj, a.smag = sc.mem.data_ptr(), sc.side.data_ptr(), sc.proj.data_ptr(), sc.smag.data_ptr()
+        a.parts, a.over = sc.parts.data_ptr(), sc.over.data_ptr()
+        check(lib().ssa_maintain(self._state(), a, stream_ptr(self.device)), "ssa_maintain")
+        if refit_all:
+            self.refits += 1
+
+    # heads rebuilt and refitted so far: the host path's counts plus the device's (reading those
+    # synchronises, as the reference's ``splits`` does)
+    @property
+    def rebuilds(self) -> int:
+        return self._rebuilds_host + (int(self._plan[4]) if self._plan is not None else 0)
+
+    @rebuilds.setter
+    def rebuilds(self, v: int) -> None:
+        self._rebuilds_host = v - (int(self._plan[4]) if self._plan is not None else 0)
+
+    @property
+    def resets(self) -> int:
+        return self._resets_host + (int(self._plan[5]) if self._plan is not None else 0)
+
+    @resets.setter
+    def resets(self, v: int) -> None:
+        self._resets_host = v
 
     def _refit(self, K: torch.Tensor) -> None:
         """Fit the clusters again on every binned key, with a fresh mean."""

@@ -41,7 +41,8 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 STRUCTS = {"ssa_attn_args_t": _lib.AttnArgs, "ssa_index_state_t": _lib.IndexState,
            "ssa_insert_args_t": _lib.InsertArgs, "ssa_select_args_t": _lib.SelectArgs,
-           "ssa_build_args_t": _lib.BuildArgs, "ssa_split_args_t": _lib.SplitArgs}
+           "ssa_build_args_t": _lib.BuildArgs, "ssa_split_args_t": _lib.SplitArgs,
+           "ssa_maint_args_t": _lib.MaintArgs}
 
 
 def test_struct_layouts_match_the_c_compiler(tmp_path):
