@@ -198,6 +198,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     }
   } else {
     // Issue the selection state's and the first page's label loads before anything waits on memory.
+    int n_act = 0, end_h = 0;
+    uint32_t touch = 0;
+    if constexpr (SELECT) {
+      n_act = a.st.n_c[h];
+      end_h = a.st.end[h];
+    }
     SelPre<D> pre;
     if constexpr (SELECT) sel_prefetch<D>(pre, head_view(a.st, h), a.st.C);
     int lbl[PER];
@@ -205,7 +211,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
         const int j = block_pos(0, u) + tid;
-        lbl[u] = j < n ? (int)labrow[j] : 0;
+        // fused mode: the labels are the state's rows of `capacity` (s_lh) entries, so the load
+        // need not wait for n (positions >= n are masked by the scan)
+        if constexpr (SELECT) lbl[u] = (int)labrow[min(j, (int)a.s_lh - 1)];
+        else lbl[u] = j < n ? (int)labrow[j] : 0;
+      }
+      // One row per eighth of this head's K and V span, read now and consumed after the rows:
+      // their address translations are then in place when the selected rows are read.
+      if (tid < 16) {
+        const int64_t span = (int64_t)max(n, 1);
+        const int p = (int)min<int64_t>((int64_t)(tid & 7) * span / 8, span - 1);
+        const T* tb = reinterpret_cast<const T*>(tid < 8 ? a.k : a.v) + (int64_t)h * (tid < 8 ? a.s_kh : a.s_vh);
+        touch = *reinterpret_cast<const uint32_t*>(tb + (int64_t)p * (tid < 8 ? a.s_kn : a.s_vn));
       }
     }
 
@@ -236,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
 
     if constexpr (SELECT) {
       // the head's selection, computed here while the label loads are in flight
-      const int n_act = a.st.n_c[h], end = a.st.end[h];
+      const int end = end_h;
       __syncthreads();
       float* wout = const_cast<float*>(a.w);
       const int64_t s_wr = a.s_wr;
@@ -405,6 +422,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
       }
     }
 
+    asm volatile("" ::"v"(touch));       // the translation touches above, long landed
     // ---- merge the lane groups of each wave ---------------------------------------------------
 #pragma unroll
     for (int o = LPR; o < 64; o <<= 1) {

@@ -541,16 +541,24 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
     // Pairwise halving tree over the C slots: tot = t[0] after t[c] += t[c + h] for h = C/2 .. 1.
     // Wave g computes head g's: lane l first folds its slots l, l+64, l+128, ... with the
     // strides >= 64 of the tree, then the strides 32 .. 1 run as shuffles. The terms are >= 0,
-    // so padding with +0 and folding from the largest stride gives the same bits as the tree
-    // over exactly C slots.
+    // so lanes past C padded with +0 give the same bits as the tree over exactly C slots.
     for (int g = wave; g < G; g += NT / 64) {
       float u[kMaxC / 64];
+      // the strides of the tree over the C slots (C a power of two): lane l holds slots l + 64 k
+      auto fold = [&](auto kc) {
+        constexpr int KC = decltype(kc)::value;
 #pragma unroll
-      for (int k = 0; k < kMaxC / 64; ++k) u[k] = (lane + 64 * k < C) ? S.z[g][lane + 64 * k] : 0.f;
+        for (int k = 0; k < KC; ++k) u[k] = (lane + 64 * k < C) ? S.z[g][lane + 64 * k] : 0.f;
 #pragma unroll
-      for (int half = kMaxC / 128; half >= 1; half >>= 1)
+        for (int half = KC / 2; half >= 1; half >>= 1)
 #pragma unroll
-        for (int k = 0; k < half; ++k) u[k] = u[k] + u[k + half];
+          for (int k = 0; k < half; ++k) u[k] = u[k] + u[k + half];
+      };
+      if (C > 512) fold(std::integral_constant<int, 16>{});
+      else if (C > 256) fold(std::integral_constant<int, 8>{});
+      else if (C > 128) fold(std::integral_constant<int, 4>{});
+      else if (C > 64) fold(std::integral_constant<int, 2>{});
+      else fold(std::integral_constant<int, 1>{});
       // strides 32 and 16 by shuffles, 8 .. 1 by DPP row_shl (lane l reads lane l + h of its
       // row); only lanes below the stride keep meaningful sums
       float v = u[0];
