@@ -102,6 +102,9 @@ typedef struct ssa_index_state {
   int32_t* mem; float* proj; int32_t* side; float* smag;   /* [n_heads, ms] split scratch */
   int32_t* stage;           /* [n_heads, SSA_STAGE_WORDS] insertion staged by ssa_sparse_step's
                                insert-ahead workgroup, committed by the head's last workgroup */
+  float* knbuf;             /* [n_heads, kn_rows, d] split scratch: the unit directions of the members of
+                               a cluster being split, computed once per split (NULL: recomputed per pass) */
+  int32_t kn_rows;          /* members knbuf holds per head; larger clusters recompute */
 } ssa_index_state_t;
 
 #define SSA_STAGE_WORDS 80  /* 8 header words + up to 256 int8 direction values */

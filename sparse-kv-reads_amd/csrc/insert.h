@@ -27,7 +27,10 @@ struct SplitTile {
   int tside[kTileFloats / 8];
 };
 
+constexpr int kRankLds = 512;   // members whose projections a lopsided split ranks from LDS
+
 struct InsertBase {
+  float rank_proj[kRankLds];
   float mu[kMaxD], kr[kMaxD], kn[kMaxD], sd[kMaxD];
   float va[kMaxD], vb[kMaxD], vs[kMaxD];
   float red_f[kW];
@@ -174,7 +177,7 @@ __device__ __forceinline__ bool keys_vec16(const Keys& K) {
   return (reinterpret_cast<uintptr_t>(K.base) & 15) == 0 && ((K.s_kn * es) & 15) == 0;
 }
 
-// Canonical dots over one member's key row, two 8-element chunks loaded per round. With
+// Canonical dots over one member's key row, eight 8-element chunks loaded per round. With
 // unit, kn = (K(pos, i) - mu[i]) / magc is dotted with each of the NV vectors v[0..NV);
 // otherwise out[0] = dot(kr, kr) with kr = K(pos, i) - mu[i].
 template <int NV, bool UNIT>
@@ -186,13 +189,13 @@ __device__ __forceinline__ void member_dots(const Keys& K, bool v16, int pos, co
 #pragma unroll
     for (int j = 0; j < 8; ++j) c[k][j] = 0.f;
 #pragma unroll 1
-  for (int i0 = 0; i0 < d; i0 += 16) {
-    float x[2][8];
+  for (int i0 = 0; i0 < d; i0 += 64) {
+    float x[8][8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 8; ++u)
       if (i0 + 8 * u < d) load8(K, v16, pos, i0 + 8 * u, x[u]);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < 8; ++u) {
       if (i0 + 8 * u < d) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -205,6 +208,39 @@ __device__ __forceinline__ void member_dots(const Keys& K, bool v16, int pos, co
           } else {
             c[0][j] = __builtin_fmaf(kr, kr, c[0][j]);
           }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) out[k] = ((c[k][0] + c[k][1]) + (c[k][2] + c[k][3])) + ((c[k][4] + c[k][5]) + (c[k][6] + c[k][7]));
+}
+
+// The same dots over a member's staged unit direction (H.kn row j), for splits whose members'
+// directions were computed once: the values are those member_dots computes, so are the dots.
+template <int NV>
+__device__ __forceinline__ void kn_dots(const Head& H, int j, const float* const (&v)[NV], int d, float (&out)[NV]) {
+  float c[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c[k][e] = 0.f;
+  const float* r = H.kn + (int64_t)j * d;
+#pragma unroll 1
+  for (int i0 = 0; i0 < d; i0 += 32) {
+    float4 x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + 4 * u < d) x[u] = reinterpret_cast<const float4*>(r + i0)[u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (i0 + 4 * u < d) {
+        const float xs[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = i0 + 4 * u + e;
+#pragma unroll
+          for (int k = 0; k < NV; ++k) c[k][(4 * u + e) & 7] = __builtin_fmaf(xs[e], v[k][i], c[k][(4 * u + e) & 7]);
         }
       }
     }
@@ -255,7 +291,7 @@ struct MemberTile {
 constexpr int kSumBlock = 16;
 template <class SM>
 __device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K, bool v16, int m, float* s0_out,
-                                            float* s1_out, int& n1_out) {
+                                            float* s1_out, int& n1_out, bool staged = false) {
   const int tid = threadIdx.x, d = H.d, cpr = d / 8;
   const int nbr = kTileFloats / (2 * d);
   float* part = S.u.spl.tile;                        // [2][nbr][d]
@@ -268,16 +304,41 @@ __device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K,
       float a0[8], a1[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) { a0[e] = 0.f; a1[e] = 0.f; }
-#pragma unroll 2
-      for (int j = jb; j < je; ++j) {
-        float x[8];
-        load8(K, v16, H.mem[j], i0, x);
-        const float magc = fmaxf(H.smag[j], 1e-12f);
-        const bool one = H.side[j] != 0;
+      if (staged) {
+        // the members' unit directions, staged: 8 members' chunks in flight, added in member order
+        for (int jb8 = jb; jb8 < je; jb8 += 8) {
+          float4 xa[8], xb[8];
+          bool one[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kn = (x[e] - S.mu[i0 + e]) / magc;
-          if (one) a1[e] = a1[e] + kn; else a0[e] = a0[e] + kn;
+          for (int t = 0; t < 8; ++t) {
+            const float* r = H.kn + (int64_t)min(jb8 + t, je - 1) * d + i0;
+            xa[t] = reinterpret_cast<const float4*>(r)[0];
+            xb[t] = reinterpret_cast<const float4*>(r)[1];
+            one[t] = H.side[min(jb8 + t, je - 1)] != 0;
+          }
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            if (jb8 + t < je) {
+              const float kn[8] = {xa[t].x, xa[t].y, xa[t].z, xa[t].w, xb[t].x, xb[t].y, xb[t].z, xb[t].w};
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                if (one[t]) a1[e] = a1[e] + kn[e]; else a0[e] = a0[e] + kn[e];
+              }
+            }
+          }
+        }
+      } else {
+#pragma unroll 2
+        for (int j = jb; j < je; ++j) {
+          float x[8];
+          load8(K, v16, H.mem[j], i0, x);
+          const float magc = fmaxf(H.smag[j], 1e-12f);
+          const bool one = H.side[j] != 0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float kn = (x[e] - S.mu[i0 + e]) / magc;
+            if (one) a1[e] = a1[e] + kn; else a0[e] = a0[e] + kn;
+          }
         }
       }
 #pragma unroll
@@ -304,23 +365,24 @@ __device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K,
 
 // side_j = kn_j.b > kn_j.a for every member (canonical dots), stored in H.side; returns #side 1.
 template <class SM>
-__device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K, bool v16, int m, bool with_proj) {
+__device__ __forceinline__ int member_sides(SM& S, const Head& H, const Keys& K, bool v16, int m, bool with_proj,
+                                            bool staged = false) {
   const int tid = threadIdx.x, d = H.d;
   int n1 = 0;
   for (int j = tid; j < m; j += kT) {
-    const int pos = H.mem[j];
-    const float magc = fmaxf(H.smag[j], 1e-12f);
     int one;
     if (with_proj) {
       const float* const v[3] = {S.va, S.vb, S.vs};
       float o[3];
-      member_dots<3, true>(K, v16, pos, S.mu, magc, v, d, o);
+      if (staged) kn_dots<3>(H, j, v, d, o);
+      else member_dots<3, true>(K, v16, H.mem[j], S.mu, fmaxf(H.smag[j], 1e-12f), v, d, o);
       one = o[1] > o[0] ? 1 : 0;
       H.proj[j] = o[2];
     } else {
       const float* const v[2] = {S.va, S.vb};
       float o[2];
-      member_dots<2, true>(K, v16, pos, S.mu, magc, v, d, o);
+      if (staged) kn_dots<2>(H, j, v, d, o);
+      else member_dots<2, true>(K, v16, H.mem[j], S.mu, fmaxf(H.smag[j], 1e-12f), v, d, o);
       one = o[1] > o[0] ? 1 : 0;
     }
     H.side[j] = one;
@@ -405,42 +467,80 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
     H.smag[j] = sqrtf(sq[0]);
   }
   __syncthreads();
+  // With room in the state, every member's unit direction (k - mu) / max(|k - mu|, 1e-12) is
+  // computed once here and read by the passes below, which otherwise divide every element again.
+  const bool staged = H.kn && m <= H.kn_rows;
+  if (staged) {
+    const int cpr = d / 8, nq = m * cpr;
+    for (int q0 = tid; q0 < nq; q0 += 4 * kT) {
+      float x[4][8], magc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {                   // four chunks' loads in flight
+        const int q = min(q0 + t * kT, nq - 1);
+        load8(K, v16, H.mem[q / cpr], 8 * (q % cpr), x[t]);
+        magc[t] = fmaxf(H.smag[q / cpr], 1e-12f);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int q = q0 + t * kT;
+        if (q < nq) {
+          const int j = q / cpr, i0 = 8 * (q % cpr);
+          float u[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) u[e] = (x[t][e] - S.mu[i0 + e]) / magc[t];
+          float4* r = reinterpret_cast<float4*>(H.kn + (int64_t)j * d + i0);
+          r[0] = make_float4(u[0], u[1], u[2], u[3]);
+          r[1] = make_float4(u[4], u[5], u[6], u[7]);
+        }
+      }
+    }
+    __syncthreads();
+  }
   // 3. start from the first member and the member least similar to it
-  if (tid < d) S.va[tid] = (K(H.mem[0], tid) - S.mu[tid]) / fmaxf(H.smag[0], 1e-12f);
+  if (tid < d) S.va[tid] = staged ? H.kn[tid] : (K(H.mem[0], tid) - S.mu[tid]) / fmaxf(H.smag[0], 1e-12f);
   __syncthreads();
   float lo = 0.f;
   int far = -1;
   for (int j = tid; j < m; j += kT) {
     const float* const v[1] = {S.va};
     float o[1];
-    member_dots<1, true>(K, v16, H.mem[j], S.mu, fmaxf(H.smag[j], 1e-12f), v, d, o);
+    if (staged) kn_dots<1>(H, j, v, d, o);
+    else member_dots<1, true>(K, v16, H.mem[j], S.mu, fmaxf(H.smag[j], 1e-12f), v, d, o);
     argmin_merge(lo, far, o[0], j);
   }
   block_argmin(S, lo, far);
-  if (tid < d) S.vb[tid] = (K(H.mem[far], tid) - S.mu[tid]) / fmaxf(H.smag[far], 1e-12f);
+  if (tid < d)
+    S.vb[tid] = staged ? H.kn[(int64_t)far * d + tid] : (K(H.mem[far], tid) - S.mu[tid]) / fmaxf(H.smag[far], 1e-12f);
   __syncthreads();
   // 4. 2-means on cosine similarity, 4 iterations
   int n1 = 0;
   for (int it = 0; it < 4; ++it) {
-    member_sides(S, H, K, v16, m, false);
+    member_sides(S, H, K, v16, m, false, staged);
     __syncthreads();
-    member_sums(S, H, K, v16, m, S.kr, S.sd, n1);
+    member_sums(S, H, K, v16, m, S.kr, S.sd, n1, staged);
     if (m - n1 > 0) block_unit(S, S.kr, S.va, d);
     if (n1 > 0) block_unit(S, S.sd, S.vb, d);
   }
   // 5. final sides and projections on b - a
   if (tid < d) S.vs[tid] = S.vb[tid] - S.va[tid];
   __syncthreads();
-  n1 = member_sides(S, H, K, v16, m, true);
+  n1 = member_sides(S, H, K, v16, m, true, staged);
   const float mf = (float)m, n1f = (float)n1;
   if (n1f < 0.25f * mf || n1f > 0.75f * mf) {
     // lopsided: cut at the median projection (rank ties by member order)
     const int half = m / 2;
+    // the projections in LDS for the m^2 comparisons when they fit
+    const float* pr = H.proj;
+    if (m <= kRankLds) {
+      for (int j = tid; j < m; j += kT) S.rank_proj[j] = H.proj[j];
+      __syncthreads();
+      pr = S.rank_proj;
+    }
     for (int j = tid; j < m; j += kT) {
-      const float pj = H.proj[j];
+      const float pj = pr[j];
       int rank = 0;
       for (int i = 0; i < m; ++i) {
-        const float pi = H.proj[i];
+        const float pi = pr[i];
         rank += (pi < pj || (pi == pj && i < j)) ? 1 : 0;
       }
       H.side[j] = rank >= half ? 1 : 0;
@@ -448,7 +548,7 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
     __syncthreads();
   }
   // 6. both halves' summaries; relabel side 1
-  member_sums(S, H, K, v16, m, S.kr, S.sd, n1);
+  member_sums(S, H, K, v16, m, S.kr, S.sd, n1, staged);
   float x0 = 0.f, x1 = 0.f, y0 = INFINITY, y1 = INFINITY;
   for (int j = tid; j < m; j += kT) {
     const float mg = H.smag[j];

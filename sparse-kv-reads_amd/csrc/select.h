@@ -26,6 +26,7 @@ struct Head {
   float* sum_dir; int8_t* dir8; float* cent; int8_t* cent8;
   float* mmax; float* mmin; int32_t* count; int16_t* labels;
   int32_t* mem; float* proj; int32_t* side; float* smag;
+  float* kn; int kn_rows;   // a split's member unit directions (rows of d), when the state has room
   bool q8dirs;    // scoring reads dir8
   bool q8cent;    // insertion reads cent8
 };
@@ -46,6 +47,8 @@ __device__ __forceinline__ Head head_view(const ssa_index_state_t& st, int h) {
   H.proj = st.proj ? st.proj + (int64_t)h * st.ms : nullptr;
   H.side = st.side ? st.side + (int64_t)h * st.ms : nullptr;
   H.smag = st.smag ? st.smag + (int64_t)h * st.ms : nullptr;
+  H.kn = st.knbuf && st.kn_rows > 0 ? st.knbuf + (int64_t)h * st.kn_rows * st.d : nullptr;
+  H.kn_rows = st.knbuf ? st.kn_rows : 0;
   H.q8dirs = st.summary_bits == 8 && st.dir8;
   H.q8cent = st.summary_bits == 8 && !st.shared_dirs && st.cent8;
   return H;

@@ -46,7 +46,8 @@ class IndexState(ct.Structure):
                 ("flags", vp), ("end", vp), ("nsplit", vp),
                 ("labels", vp),
                 ("mem", vp), ("proj", vp), ("side", vp), ("smag", vp),
-                ("stage", vp)]
+                ("stage", vp),
+                ("knbuf", vp), ("kn_rows", i32)]
 
 STAGE_WORDS = 80          # SSA_STAGE_WORDS
 

@@ -55,7 +55,7 @@ class _MaintScratch:
 _MAINT: dict = {}
 
 STACKED = ("n_c", "sum_dir", "dir8", "cent", "cent8", "mmax", "mmin", "count", "ksum", "mu_ref", "rbar", "flags",
-           "cap", "vthr", "_mem", "_proj", "_side", "_smag", "_stage", "nsplit", "labels", "end_dev")
+           "cap", "vthr", "_mem", "_proj", "_side", "_smag", "_stage", "_knbuf", "nsplit", "labels", "end_dev")
 
 
 class DenseAttentionGraph:

@@ -63,6 +63,7 @@ def kmeans_init_indices(m: int, C: int, seed: int) -> torch.Tensor:
 
 class SphereIndexFused:
     BUILD_HEADS = 64          # heads (re)built per ssa_build call
+    KN_ROWS = 512             # members of a splitting cluster whose unit directions are kept (knbuf)
 
     def __init__(self, *, C: int = 256, window: int = 64, delta: float = 0.03, capacity: int = 65536,
                  check_every: int = 16, seed: int = 0, kind: str = "random", partition: str = "random",
@@ -141,6 +142,10 @@ class SphereIndexFused:
         self._side = torch.zeros(H_kv, self.MS, dtype=torch.int32, device=device)
         self._smag = torch.zeros(H_kv, self.MS, **f32)
         self._stage = torch.zeros(H_kv, STAGE_WORDS, dtype=torch.int32, device=device)
+        # unit directions of a splitting cluster's members, computed once per split (the split's
+        # passes otherwise divide every element again); clusters past KN_ROWS members recompute
+        self.kn_rows = min(self.MS, self.KN_ROWS) if self.splitting else 0
+        self._knbuf = torch.empty(H_kv, self.kn_rows, d, **f32) if self.kn_rows else None
         self._flags_host = torch.zeros(H_kv, dtype=torch.int32, pin_memory=True)
         self._pending = None
         self._w = {}
@@ -165,6 +170,7 @@ class SphereIndexFused:
         s.flags, s.end, s.nsplit, s.labels = p("flags"), p("end_dev"), p("nsplit"), p("labels")
         s.mem, s.proj, s.side, s.smag = p("_mem"), p("_proj"), p("_side"), p("_smag")
         s.stage = p("_stage")
+        s.knbuf, s.kn_rows = p("_knbuf"), self.kn_rows
         return s
 
     def _insert_args(self, K: torch.Tensor, *, n_host: int = 0, n_dev: torch.Tensor | None = None,

@@ -183,10 +183,17 @@ def test_selection_is_bit_exact_given_identical_summaries(group, budget):
         assert int((w64 != want).sum(1).max()) <= 1
 
 
-def test_in_kernel_splits_are_bit_exact_and_keep_the_cap():
+@pytest.mark.parametrize("kn_rows", [0, 8, 512])
+def test_in_kernel_splits_are_bit_exact_and_keep_the_cap(kn_rows):
+    """In-kernel splits with the members' unit directions recomputed in every pass (kn_rows 0),
+    computed once into the state's split scratch (512 rows: every cluster fits), or both (8 rows:
+    the larger clusters recompute): the same state as the oracle in each case."""
     K, V, q = _keys(3, 2600, seed=5, centers=16)
     idx = _fused(C=128, C_init=16)
     idx.observe(K, 1000)
+    if kn_rows:                                   # the scratch a splitting index allocates
+        idx.kn_rows = kn_rows
+        idx._knbuf = torch.empty(3, kn_rows, 128, device="cuda")
     canon = _canon_like(idx, K, 1000)
     cap = float(1.5 * (1000 - 17) / 16)
     idx.cap.fill_(cap)
