@@ -22,15 +22,18 @@ constexpr int kGatherRun = 32;  // consecutive label positions per thread per pa
 
 // LDS of the insertion and split code. A kernel that runs them passes a struct with the members
 // of InsertSmem (its own may add more to the union u, which must hold spl).
+constexpr int kRankLds = 512;   // members whose projections a lopsided split ranks from LDS
+static_assert(kRankLds <= kTileFloats, "the ranking reuses the tile");
+
 struct SplitTile {
-  float tile[kTileFloats];
+  union {
+    float tile[kTileFloats];
+    float rank[kRankLds];         // the lopsided split's projections (the tile is idle then)
+  };
   int tside[kTileFloats / 8];
 };
 
-constexpr int kRankLds = 512;   // members whose projections a lopsided split ranks from LDS
-
 struct InsertBase {
-  float rank_proj[kRankLds];
   float mu[kMaxD], kr[kMaxD], kn[kMaxD], sd[kMaxD];
   float va[kMaxD], vb[kMaxD], vs[kMaxD];
   float red_f[kW];
@@ -177,7 +180,7 @@ __device__ __forceinline__ bool keys_vec16(const Keys& K) {
   return (reinterpret_cast<uintptr_t>(K.base) & 15) == 0 && ((K.s_kn * es) & 15) == 0;
 }
 
-// Canonical dots over one member's key row, eight 8-element chunks loaded per round. With
+// Canonical dots over one member's key row, two 8-element chunks loaded per round. With
 // unit, kn = (K(pos, i) - mu[i]) / magc is dotted with each of the NV vectors v[0..NV);
 // otherwise out[0] = dot(kr, kr) with kr = K(pos, i) - mu[i].
 template <int NV, bool UNIT>
@@ -189,13 +192,13 @@ __device__ __forceinline__ void member_dots(const Keys& K, bool v16, int pos, co
 #pragma unroll
     for (int j = 0; j < 8; ++j) c[k][j] = 0.f;
 #pragma unroll 1
-  for (int i0 = 0; i0 < d; i0 += 64) {
-    float x[8][8];
+  for (int i0 = 0; i0 < d; i0 += 16) {
+    float x[2][8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 2; ++u)
       if (i0 + 8 * u < d) load8(K, v16, pos, i0 + 8 * u, x[u]);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 2; ++u) {
       if (i0 + 8 * u < d) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -227,13 +230,13 @@ __device__ __forceinline__ void kn_dots(const Head& H, int j, const float* const
     for (int e = 0; e < 8; ++e) c[k][e] = 0.f;
   const float* r = H.kn + (int64_t)j * d;
 #pragma unroll 1
-  for (int i0 = 0; i0 < d; i0 += 32) {
-    float4 x[8];
+  for (int i0 = 0; i0 < d; i0 += 16) {
+    float4 x[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 4; ++u)
       if (i0 + 4 * u < d) x[u] = reinterpret_cast<const float4*>(r + i0)[u];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 4; ++u) {
       if (i0 + 4 * u < d) {
         const float xs[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
 #pragma unroll
@@ -305,19 +308,19 @@ __device__ __forceinline__ void member_sums(SM& S, const Head& H, const Keys& K,
 #pragma unroll
       for (int e = 0; e < 8; ++e) { a0[e] = 0.f; a1[e] = 0.f; }
       if (staged) {
-        // the members' unit directions, staged: 8 members' chunks in flight, added in member order
-        for (int jb8 = jb; jb8 < je; jb8 += 8) {
-          float4 xa[8], xb[8];
-          bool one[8];
+        // the members' unit directions, staged: 4 members' chunks in flight, added in member order
+        for (int jb8 = jb; jb8 < je; jb8 += 4) {
+          float4 xa[4], xb[4];
+          bool one[4];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
+          for (int t = 0; t < 4; ++t) {
             const float* r = H.kn + (int64_t)min(jb8 + t, je - 1) * d + i0;
             xa[t] = reinterpret_cast<const float4*>(r)[0];
             xb[t] = reinterpret_cast<const float4*>(r)[1];
             one[t] = H.side[min(jb8 + t, je - 1)] != 0;
           }
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
+          for (int t = 0; t < 4; ++t) {
             if (jb8 + t < je) {
               const float kn[8] = {xa[t].x, xa[t].y, xa[t].z, xa[t].w, xb[t].x, xb[t].y, xb[t].z, xb[t].w};
 #pragma unroll
@@ -472,16 +475,16 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
   const bool staged = H.kn && m <= H.kn_rows;
   if (staged) {
     const int cpr = d / 8, nq = m * cpr;
-    for (int q0 = tid; q0 < nq; q0 += 4 * kT) {
-      float x[4][8], magc[4];
+    for (int q0 = tid; q0 < nq; q0 += 2 * kT) {
+      float x[2][8], magc[2];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {                   // four chunks' loads in flight
+      for (int t = 0; t < 2; ++t) {                   // two chunks' loads in flight
         const int q = min(q0 + t * kT, nq - 1);
         load8(K, v16, H.mem[q / cpr], 8 * (q % cpr), x[t]);
         magc[t] = fmaxf(H.smag[q / cpr], 1e-12f);
       }
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < 2; ++t) {
         const int q = q0 + t * kT;
         if (q < nq) {
           const int j = q / cpr, i0 = 8 * (q % cpr);
@@ -532,9 +535,9 @@ __device__ __forceinline__ void split_cluster(SM& S, const ssa_index_state_t& st
     // the projections in LDS for the m^2 comparisons when they fit
     const float* pr = H.proj;
     if (m <= kRankLds) {
-      for (int j = tid; j < m; j += kT) S.rank_proj[j] = H.proj[j];
+      for (int j = tid; j < m; j += kT) S.u.spl.rank[j] = H.proj[j];
       __syncthreads();
-      pr = S.rank_proj;
+      pr = S.u.spl.rank;
     }
     for (int j = tid; j < m; j += kT) {
       const float pj = pr[j];

@@ -9,6 +9,7 @@ linked into one shared library next to this file, which ``ssa_amd._lib`` loads.
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -35,11 +36,43 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         msg = "\n".join(line for line in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in line)
         raise RuntimeError(f"build failed: {' '.join(cmd)}\n{msg}")
+    return r.stderr
+
+
+# The step kernel's resident workgroups per compute unit. With insert-ahead its grid is one
+# workgroup per compute unit plus a stager per head, so a kernel that fits only one wave per SIMD
+# (registers or LDS) leaves the stagers waiting for a whole workgroup to finish, which lengthens
+# every step by that workgroup's runtime. The build refuses such a kernel for the caches, head
+# sizes and query groups of the decode configurations it serves (2-byte K/V, d <= 128, up to 4
+# query heads per KV head); fp32 caches hold twice the row registers and are a parity path.
+_KERNEL = re.compile(r"Function Name: _ZN3ssa13decode_kernelI(\w+?)Li(\d+)ELi(\d+)ELb(\d)ELb(\d)ELb(\d)E")
+_OCC = re.compile(r"Occupancy \[waves/SIMD\]: (\d+)")
+
+
+def decode_occupancy(remarks: str) -> dict:
+    """{(dtype, d, GMAX, dense, select, ahead): waves per SIMD} from the compiler's
+    kernel-resource-usage remarks of a decode translation unit."""
+    out = {}
+    for block in remarks.split("Function Name: ")[1:]:
+        m = _KERNEL.match("Function Name: " + block)
+        o = _OCC.search(block)
+        if m and o:
+            out[(m.group(1), int(m.group(2)), int(m.group(3)), *(int(m.group(i)) for i in (4, 5, 6)))] = int(o.group(1))
+    return out
+
+
+def _check_occupancy(remarks: str, src: str) -> None:
+    occ = decode_occupancy(remarks)
+    if not occ:
+        raise RuntimeError(f"{src}: no resource-usage remarks for decode_kernel")
+    low = {k: v for k, v in occ.items() if k[0] != "f" and k[1] <= 128 and k[2] <= 4 and v < 2}
+    if low:
+        raise RuntimeError(f"{src}: decode kernels below 2 waves per SIMD: {sorted(low)}")
 
 
 def build(verbose: bool = False) -> Path:
@@ -50,13 +83,17 @@ def build(verbose: bool = False) -> Path:
     cmds, objs = [], []
     for src, extra in SOURCES.items():
         obj = objdir / (src.replace(".hip", ".o"))
-        cmds.append([hipcc, *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)])
+        remarks = ["-Rpass-analysis=kernel-resource-usage"] if src.startswith("decode_") else []
+        cmds.append([hipcc, *COMMON, *extra, *remarks, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
         if verbose:
             print(" ".join(cmds[-1]), flush=True)
     jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with ThreadPoolExecutor(jobs) as pool:
-        list(pool.map(_run, cmds))
+        logs = list(pool.map(_run, cmds))
+    for src, log in zip(SOURCES, logs):
+        if src.startswith("decode_"):
+            _check_occupancy(log, src)
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, "-shared", f"--offload-arch={ARCH}", *objs, "-o", str(tmp)])
     os.replace(tmp, LIB)
