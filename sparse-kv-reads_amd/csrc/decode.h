@@ -107,7 +107,9 @@ __device__ __forceinline__ void store_out(void* out, int dt, int64_t i, float x)
 }
 
 constexpr int kMaxS = 256;           // splits per head (host clamps)
-constexpr int kMergeBatch = 8;       // accumulator loads (float4) each merging thread issues at once
+// accumulator loads (float4) each merging thread issues at once: S = 32 splits of G x 128
+// columns in one round up to G = 4
+template <int GMAX> constexpr int merge_batch() { return GMAX >= 4 ? 16 : 8; }
 
 // Agent-scope relaxed load: coherent with the agent-scope stores of other workgroups on any XCD.
 __device__ __forceinline__ float load_coherent(const float* p) {
@@ -145,6 +147,7 @@ struct DecodeSmem {
   float gden[GMAX];
   int red_i[kWaves];
   int last;
+  int stage_hdr[9];                                  // the staged insertion's header (commit)
 };
 
 // DENSE: every position in [0, n) is read with weight 1. Otherwise positions are selected by
@@ -483,10 +486,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   }
   __syncthreads();
   if (!sm.last) return;
+  // the staged insertion's words load beside the partials' (the stager's stores were
+  // acknowledged before it counted in)
+  StagePre stp;
+  if constexpr (AHEAD) stage_prefetch<D>(stp, a.st, h);
   // ---- the last workgroup of head h merges the S partials ----------------------------------
   // One round of loads, all issued before the first wait: in wave 0, every split's (max, sum)
   // and row count spread over the lanes, first, so that the rescale factors can be computed
-  // while the rest arrives; then this thread's accumulator columns (up to kMergeBatch splits)
+  // while the rest arrives; then this thread's accumulator columns (up to MB splits)
   // into registers. The partials are read with agent-scope loads (coherent across XCDs), so no
   // L2 invalidate is needed.
   const int64_t hb = (int64_t)h * S;
@@ -518,9 +525,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
       cpart += __hip_atomic_load(a.part_cnt + hb + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // branchless: out-of-range splits re-read split S-1 and get weight 0 below
-  float4 va[kMergeBatch];
+  constexpr int MB = merge_batch<GMAX>();
+  float4 va[MB];
 #pragma unroll
-  for (int k = 0; k < kMergeBatch; ++k) {
+  for (int k = 0; k < MB; ++k) {
     const int s2 = min(sg0 + k * nsg0, S - 1);
     va[k] = load_coherent4(pa + ((int64_t)s2 * cols4 + col0) * 4);
   }
@@ -560,13 +568,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
       int s2 = sg;
       if (c0 == 0) {                 // the batch already in registers
 #pragma unroll
-        for (int k = 0; k < kMergeBatch; ++k) {
+        for (int k = 0; k < MB; ++k) {
           const int sk = sg + k * nsg;
           const float f = sk < S ? sm.u.mrg.f[min(sk, S - 1) * G + g] : 0.f;
           acc4.x = fmaf(f, va[k].x, acc4.x); acc4.y = fmaf(f, va[k].y, acc4.y);
           acc4.z = fmaf(f, va[k].z, acc4.z); acc4.w = fmaf(f, va[k].w, acc4.w);
         }
-        s2 = sg + kMergeBatch * nsg;
+        s2 = sg + MB * nsg;
       }
 #pragma unroll 8
       for (; s2 < S; s2 += nsg) {
@@ -603,8 +611,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     // in after its scan, the stager after its stores), so the state may now move to the next
     // step: commit the staged insertion of the keys that leave the window at length n + 1, as
     // ssa_insert would bin them at the start of the next step.
+    stage_publish(stp, sm.stage_hdr);
     __syncthreads();                                     // the merge is done with sm.u
-    insert_commit<D>(sm.u.tail, a.st, a.ins, h, n + 1);
+    insert_commit<D>(sm.u.tail, a.st, a.ins, h, n + 1, stp, sm.stage_hdr);
   }
 }
 

@@ -885,15 +885,38 @@ __device__ __forceinline__ void insert_stage(SM& S, const ssa_index_state_t& st,
   }
 }
 
+// The staged words of head h, loaded by the committing workgroup as soon as it knows it commits
+// (with the merge's loads, so that the commit does not wait for another round trip): header word
+// threadIdx.x in the first 9 threads, word threadIdx.x of the int8 direction row in the first
+// D/4. stage_publish puts the header into hdr (LDS) for every thread; a barrier must follow.
+struct StagePre {
+  int hw, d8w;
+};
+
+template <int D>
+__device__ __forceinline__ void stage_prefetch(StagePre& T, const ssa_index_state_t& st, int h) {
+  const int32_t* stg = st.stage + (int64_t)h * kStageWords;
+  const int t = threadIdx.x;
+  T.hw = t < 9 ? stage_get(stg, t) : 0;
+  T.d8w = t < D / 4 ? stage_get(stg, kStageHead + t) : 0;
+}
+
+__device__ __forceinline__ void stage_publish(const StagePre& T, int* hdr) {
+  if (threadIdx.x < 9) hdr[threadIdx.x] = T.hw;
+}
+
 // Commit what insert_stage staged for head h (called by the head's last workgroup, after every
-// workgroup of the step has read the state). A kStageGeneral stage runs the whole insertion.
+// workgroup of the step has read the state; T and hdr hold stage_prefetch's words). A
+// kStageGeneral stage runs the whole insertion.
 template <int D, class SM>
 __device__ __forceinline__ void insert_commit(SM& S, const ssa_index_state_t& st, const ssa_insert_args_t& in, int h,
-                                              int n) {
+                                              int n, const StagePre& T, const int* hdr) {
   const int tid = threadIdx.x;
   const Head H = head_view(st, h);
-  const int32_t* stg = st.stage + (int64_t)h * kStageWords;
-  const int status = stage_get(stg, 0);
+  int Th[9];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) Th[i] = hdr[i];
+  const int status = Th[0];
   if (status == kStageGeneral) {
     InsPre<D> P;
     insert_prefetch<D>(P, st, in, h, n);
@@ -901,10 +924,10 @@ __device__ __forceinline__ void insert_commit(SM& S, const ssa_index_state_t& st
     return;
   }
   if (status != kStageOne && status != kStageSplit) return;
-  const int row = stage_get(stg, 1), p = stage_get(stg, 2), new_end = stage_get(stg, 3);
-  const int cn = stage_get(stg, 4), n_act = stage_get(stg, 7), flags = stage_get(stg, 8);
-  const float mx = __int_as_float(stage_get(stg, 5)), mn = __int_as_float(stage_get(stg, 6));
-  if (tid < D / 4) reinterpret_cast<int*>(H.dir8 + (int64_t)row * D)[tid] = stage_get(stg, kStageHead + tid);
+  const int row = Th[1], p = Th[2], new_end = Th[3];
+  const int cn = Th[4], n_act = Th[7], flags = Th[8];
+  const float mx = __int_as_float(Th[5]), mn = __int_as_float(Th[6]);
+  if (tid < D / 4) reinterpret_cast<int*>(H.dir8 + (int64_t)row * D)[tid] = T.d8w;
   if (tid == 0) {
     H.mmax[row] = mx;
     H.mmin[row] = mn;

@@ -411,66 +411,67 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
       for (int g = 0; g < GMAX; ++g) z[k][g] = -INFINITY;
       continue;
     }
-    float nrm2_i[8], dot_i[8][GMAX];
     const int kact = min(C, n_act);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (256 * k + 32 * i >= kact) {            // rows [256k + 32i, +32) hold no slot in use (uniform)
-        nrm2_i[i] = 0.f;
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g) dot_i[i][g] = 0.f;
-        continue;
-      }
-      const int cr = min(grp + 256 * k + 32 * i, C - 1);        // rows past C are never kept
-      float x[E];
-      if (H.q8dirs) {
-        int4 raw[(E + 15) / 16 + (E < 16 ? 1 : 0)];
-        const int8_t* bytes;
-        if (k == 0) {
-          bytes = reinterpret_cast<const int8_t*>(P.raw) + i * E;
-        } else {
-          load_chunk8<D>(H.dir8 + (int64_t)cr * D, jl, raw, 0);
-          bytes = reinterpret_cast<const int8_t*>(raw);
-        }
-#pragma unroll
-        for (int e = 0; e < E; ++e) x[e] = (float)bytes[e];
-      } else {
-        const float* rp = H.sum_dir + (int64_t)cr * D + jl * E;
-#pragma unroll
-        for (int e = 0; e < E; ++e) x[e] = rp[e];
-      }
-      float cn = 0.f, cq[GMAX];
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g) cq[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        cn = __builtin_fmaf(x[e], x[e], cn);
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g)
-          cq[g] = __builtin_fmaf(QREG ? qv[QREG ? g : 0][QREG ? e : 0] : S.q[g][jl * E + e], x[e], cq[g]);
-      }
-      nrm2_i[i] = group8_sum(cn);
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g) dot_i[i][g] = group8_sum(cq[g]);
-    }
-    // lane j keeps row i = j of the round
-    float nrm2 = nrm2_i[0], dot[GMAX];
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) dot[g] = dot_i[0][g];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) {
-      nrm2 = jl == i ? nrm2_i[i] : nrm2;
-#pragma unroll
-      for (int g = 0; g < GMAX; ++g) dot[g] = jl == i ? dot_i[i][g] : dot[g];
-    }
     const int c = sel_slot(tid, k);
     const bool used = c < C && c < n_act;
+    // this round's summaries and rows (the first round's were prefetched), the rows in batches of
+    // RB whose loads are all issued before the first dot of the batch waits on one (RB = 8 with
+    // two query heads per KV head; 4 otherwise, which keeps the kernel at two waves per SIMD)
+    constexpr int RB = GMAX == 2 ? 8 : 4;
     float mx = 0.f, mn = 0.f;
     int ct = 0;
     if (k == 0) {
       ct = P.cnt; mx = P.mx; mn = P.mn;
     } else if (used) {
       ct = H.count[c]; mx = H.mmax[c]; mn = H.mmin[c];
+    }
+    // lane j keeps the dots of row i = j of the round (every lane of a group gets each total)
+    float nrm2 = 0.f, dot[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) dot[g] = 0.f;
+#pragma unroll
+    for (int i0 = 0; i0 < 8; i0 += RB) {
+      int4 rk[(E * RB + 15) / 16];             // the batch's chunks, E bytes each, packed
+      if (k > 0 && H.q8dirs) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+          if (256 * k + 32 * (i0 + i) < kact)
+            load_chunk8<D>(H.dir8 + (int64_t)min(grp + 256 * k + 32 * (i0 + i), C - 1) * D, jl, rk, i);
+      }
+#pragma unroll
+      for (int i1 = 0; i1 < RB; ++i1) {
+        const int i = i0 + i1;
+        if (256 * k + 32 * i >= kact) continue;  // rows [256k + 32i, +32) hold no slot in use (uniform)
+        const int cr = min(grp + 256 * k + 32 * i, C - 1);      // rows past C are never kept
+        float x[E];
+        if (H.q8dirs) {
+          const int8_t* bytes = k == 0 ? reinterpret_cast<const int8_t*>(P.raw) + i * E
+                                       : reinterpret_cast<const int8_t*>(rk) + i1 * E;
+#pragma unroll
+          for (int e = 0; e < E; ++e) x[e] = (float)bytes[e];
+        } else {
+          const float* rp = H.sum_dir + (int64_t)cr * D + jl * E;
+#pragma unroll
+          for (int e = 0; e < E; ++e) x[e] = rp[e];
+        }
+        float cn = 0.f, cq[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) cq[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          cn = __builtin_fmaf(x[e], x[e], cn);
+#pragma unroll
+          for (int g = 0; g < GMAX; ++g)
+            cq[g] = __builtin_fmaf(QREG ? qv[QREG ? g : 0][QREG ? e : 0] : S.q[g][jl * E + e], x[e], cq[g]);
+        }
+        cn = group8_sum(cn);
+        nrm2 = jl == i ? cn : nrm2;
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+          const float t = group8_sum(cq[g]);
+          dot[g] = jl == i ? t : dot[g];
+        }
+      }
     }
     cnt[k] = used && ct > 0 ? ct : 0;
     const float nrm = fmaxf(sqrtf(nrm2), 1e-12f);
