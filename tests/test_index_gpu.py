@@ -183,6 +183,30 @@ def test_selection_is_bit_exact_given_identical_summaries(group, budget):
         assert int((w64 != want).sum(1).max()) <= 1
 
 
+@pytest.mark.parametrize("group", ["sum_share", "per_head", "max", "max_rel"])
+@pytest.mark.parametrize("H", [8, 16])
+def test_selection_past_256_clusters_is_bit_exact(group, H):
+    """Scoring runs in rounds of 256 slots: with 520 clusters fitted (rounds 0, 1 and a partial
+    round 2), the standalone selection and the fused step's own selection both equal the
+    oracle's, at two and four query heads per KV head."""
+    n = 4096
+    K, V, q = _keys(4, n, d=64, H=H, seed=31, centers=128)
+    idx = _fused(C=1024, C_init=520, window=16, capacity=n + 64, check_every=10 ** 9)
+    idx.observe(K, n)
+    canon = CanonIndex.from_gpu(idx)
+    assert int(canon.n_c.min()) == 520
+    for budget in (0.05, 0.2):
+        _, w = idx.labels_and_weights(q, n=n, budget=budget, group=group)
+        want = canon.select(q, budget=budget, group=group)
+        assert np.array_equal(w.cpu().numpy(), want)
+    out, labels, w = idx.attend(q, K, V, n=n, budget=0.2, group=group)
+    torch.cuda.synchronize()
+    assert np.array_equal(w.cpu().numpy(), canon.select(q, budget=0.2, group=group))
+    want = ref.label_weighted_attention(q.double().cpu().numpy(), K.double().cpu().numpy(),
+                                        V.double().cpu().numpy(), canon.labels[:, :n], w.cpu().numpy())
+    np.testing.assert_allclose(out.double().cpu().numpy(), want, rtol=0, atol=2e-2)
+
+
 @pytest.mark.parametrize("kn_rows", [0, 8, 512])
 def test_in_kernel_splits_are_bit_exact_and_keep_the_cap(kn_rows):
     """In-kernel splits with the members' unit directions recomputed in every pass (kn_rows 0),
