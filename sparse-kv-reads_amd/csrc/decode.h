@@ -58,7 +58,7 @@ constexpr int kWaves = kThreads / 64;
 // positions compacted per pass: the selected-row list (position + GMAX weights per row) lives in
 // LDS, so the page shrinks as the weight rows grow
 template <int GMAX> constexpr int page_size() { return GMAX <= 4 ? 2048 : 1024; }
-constexpr int kMaxW = 1025;          // weight slots (C + 1) held in LDS per row
+constexpr int kMaxW = kMaxC + 1;     // weight slots (C + 1) held in LDS per row
 
 template <int LPR>
 __device__ __forceinline__ float row_sum(float x) {
@@ -124,17 +124,18 @@ __device__ __forceinline__ float4 load_coherent4(const float* p) {
                      __uint_as_float((unsigned int)b), __uint_as_float((unsigned int)(b >> 32)));
 }
 
-template <int D, int GMAX, bool DENSE>
+// CMAX: the largest slot count of the fused selection (256 or 1024); the weight rows hold CMAX + 1
+template <int D, int GMAX, bool DENSE, int CMAX = kMaxC>
 struct DecodeSmem {
   static constexpr int kPage = page_size<GMAX>();
   static constexpr int kSelG = DENSE ? 1 : GMAX;
-  float lw[DENSE ? 1 : GMAX][DENSE ? 1 : kMaxW];       // log2 w per weight row, -inf where w <= 0
+  float lw[DENSE ? 1 : GMAX][DENSE ? 1 : CMAX + 1];    // log2 w per weight row, -inf where w <= 0
   union {
     struct {
       int pos[DENSE ? 1 : kPage];                        // selected positions of the current page
       float rlw[GMAX][DENSE ? 1 : kPage];                // their log2 w per weight row
     } list;
-    SelSmem<kSelG> sel;                                  // fused selection scratch
+    SelSmem<kSelG, CMAX> sel;                            // fused selection scratch
     InsertSmem tail;                                     // fused insertion ahead
     struct {
       float f[kMaxS * GMAX];                             // rescale factor per (split, head)
@@ -154,7 +155,7 @@ struct DecodeSmem {
 // w[label] > 0 (any query head of the group, when w has one row per query head). SELECT: w is
 // not read but computed by this workgroup from the index state (select.h), the same bits the
 // selection kernel writes; workgroup 0 of each head also stores it.
-template <typename T, int D, int GMAX, bool DENSE, bool SELECT = false, bool AHEAD = false>
+template <typename T, int D, int GMAX, bool DENSE, bool SELECT = false, bool AHEAD = false, int CMAX = kMaxC>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   constexpr int LPR = D / 8;           // lanes per row
   constexpr int RPI = 64 / LPR;        // rows per wave instruction
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   constexpr int kPage = page_size<GMAX>();
   constexpr int PER = kPage / kThreads;
   using Raw = typename RawRow<T>::type;
-  __shared__ DecodeSmem<D, GMAX, DENSE> sm;
+  __shared__ DecodeSmem<D, GMAX, DENSE, CMAX> sm;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane / LPR, li = lane % LPR;
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
       float* wout = const_cast<float*>(a.w);
       const int64_t s_wr = a.s_wr;
       const bool store_w = sp == 0 && wout != nullptr;
-      select_head<D, kThreads, GMAX>(sm.u.sel, head_view(a.st, h), pre, a.st.C, n_act, end, G, a.budget, a.group,
+      select_head<D, kThreads, GMAX, CMAX>(sm.u.sel, head_view(a.st, h), pre, a.st.C, n_act, end, G, a.budget, a.group,
                                      a.sel_scale, [&](int r, int c, float x) {
                                        sm.lw[r][c] = x > 0.f ? 0.f : -INFINITY;
                                        if (store_w) wout[(int64_t)(per_head ? h * G + r : h) * s_wr + c] = x;
@@ -270,14 +271,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
       const int nrow = per_head ? G : 1;
       for (int r = 0; r < nrow; ++r) {
         const float* wr = a.w + (int64_t)(per_head ? h * G + r : h) * a.s_wr;
-        float x[(kMaxW + kThreads - 1) / kThreads];
+        float x[(CMAX + kThreads) / kThreads];
 #pragma unroll
-        for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
+        for (int k = 0; k < (CMAX + kThreads) / kThreads; ++k) {
           const int c = tid + k * kThreads;
           x[k] = c < a.w_len ? wr[c] : 0.f;
         }
 #pragma unroll
-        for (int k = 0; k < (kMaxW + kThreads - 1) / kThreads; ++k) {
+        for (int k = 0; k < (CMAX + kThreads) / kThreads; ++k) {
           const int c = tid + k * kThreads;
           if (c < a.w_len) sm.lw[r][c] = x[k] > 0.f ? __log2f(x[k]) : -INFINITY;
         }
@@ -620,12 +621,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
 enum Mode { kDense = 0, kLabelled = 1, kFused = 2, kFusedAhead = 3 };
 
 
+// Slot counts up to 256 (one scoring round) have their own fused kernels at d = 128: the selection's
+// per-slot registers, LDS and code then cover 256 slots instead of 1024.
 template <typename T, int D, int GMAX>
 hipError_t launch_decode_t(const DecodeParams& p, int mode, hipStream_t st) {
   dim3 grid(p.S + (mode == kFusedAhead ? 1 : 0), p.n_heads);
+  const bool small = D == 128 && p.st.C <= 256;
   if (mode == kDense) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, true>), grid, dim3(kThreads), 0, st, p);
   else if (mode == kLabelled) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false>), grid, dim3(kThreads), 0, st, p);
+  else if (mode == kFused && small)
+    hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true, false, (D == 128 ? 256 : kMaxC)>), grid, dim3(kThreads), 0, st, p);
   else if (mode == kFused) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true>), grid, dim3(kThreads), 0, st, p);
+  else if (small)
+    hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true, true, (D == 128 ? 256 : kMaxC)>), grid, dim3(kThreads), 0, st, p);
   else hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false, true, true>), grid, dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }

@@ -178,17 +178,19 @@ __device__ __forceinline__ void row_dots(const float* r, const float (*q0)[kMaxD
 
 constexpr int kBins = 1024;     // threshold buckets of the selection (top 10 bits of the rank key)
 
-template <int GMAX>
+// CMAX: the largest slot count the selection is compiled for (a power of two, 256 or 1024); the
+// per-slot arrays, the scoring rounds and the denominator tree are sized by it.
+template <int GMAX, int CMAX = kMaxC>
 struct SelSmem {
   float q[GMAX][kMaxD];             // the group's query rows, fp32
-  float z[GMAX][kMaxC];             // softmax terms, for the denominator tree
+  float z[GMAX][CMAX];              // softmax terms, for the denominator tree
   float tree[GMAX];                 // softmax denominators
   float red[GMAX][16];              // per-wave maxima
   int hist[kBins];                  // keys per bucket
   int wsum[16];                     // per-wave bucket totals
   int bstar, base, nlist;           // crossing bucket, keys ranked before it, its member count
-  unsigned long long lrk[kMaxC];    // rank keys of the crossing bucket's clusters
-  int lcnt[kMaxC];                  // and their key counts
+  unsigned long long lrk[CMAX];     // rank keys of the crossing bucket's clusters
+  int lcnt[CMAX];                   // and their key counts
 };
 
 // The state a thread scores first (slot threadIdx.x), loaded at kernel start so that its
@@ -280,8 +282,8 @@ __device__ __forceinline__ unsigned long long rank_key(float key, int c) {
 //     counted exactly.
 // If all keys together are fewer than need, every live cluster is taken.
 // On entry S.hist is zero and S.nlist is 0; both are so again on return.
-template <int NT, int KPT, int GMAX, typename Emit>
-__device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)[KPT], const int (&cnt)[KPT], int C,
+template <int NT, int KPT, class SS, typename Emit>
+__device__ __forceinline__ void bucket_take(SS& S, const float (&key)[KPT], const int (&cnt)[KPT], int C,
                                             int64_t need, unsigned int base, int shift, int row, Emit emit) {
   static_assert(kBins == 4 * NT, "one int4 of buckets per thread");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -371,10 +373,11 @@ __device__ __forceinline__ void bucket_take(SelSmem<GMAX>& S, const float (&key)
 // slot c in [0, C] of every weight row (one row, or G rows for per_head); slot C, the
 // always-read exact set, gets 1. Each thread scores slots threadIdx.x + k * NT and keeps their
 // scores in registers.
-template <int D, int NT, int GMAX, typename Emit>
-__device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, const SelPre<D>& P, int C, int n_act, int end, int G,
-                            double budget, int group, float scale, Emit emit) {
-  constexpr int KPT = kMaxC / NT;
+template <int D, int NT, int GMAX, int CMAX = kMaxC, typename Emit>
+__device__ __forceinline__ void select_head(SelSmem<GMAX, CMAX>& S, const Head& H, const SelPre<D>& P, int C, int n_act,
+                                            int end, int G, double budget, int group, float scale, Emit emit) {
+  static_assert(CMAX % NT == 0 && CMAX >= 64, "whole rounds of slots");
+  constexpr int KPT = CMAX / NT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool per_head = group == 1;
   const int nrows = per_head ? G : 1;
@@ -547,7 +550,7 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
     // strides >= 64 of the tree, then the strides 32 .. 1 run as shuffles. The terms are >= 0,
     // so lanes past C padded with +0 give the same bits as the tree over exactly C slots.
     for (int g = wave; g < G; g += NT / 64) {
-      float u[kMaxC / 64];
+      float u[CMAX / 64];
       // the strides of the tree over the C slots (C a power of two): lane l holds slots l + 64 k
       auto fold = [&](auto kc) {
         constexpr int KC = decltype(kc)::value;
@@ -558,11 +561,18 @@ __device__ __forceinline__ void select_head(SelSmem<GMAX>& S, const Head& H, con
 #pragma unroll
           for (int k = 0; k < half; ++k) u[k] = u[k] + u[k + half];
       };
-      if (C > 512) fold(std::integral_constant<int, 16>{});
-      else if (C > 256) fold(std::integral_constant<int, 8>{});
-      else if (C > 128) fold(std::integral_constant<int, 4>{});
-      else if (C > 64) fold(std::integral_constant<int, 2>{});
-      else fold(std::integral_constant<int, 1>{});
+      bool folded = false;
+      if constexpr (CMAX > 512) {
+        if (C > 512) { fold(std::integral_constant<int, 16>{}); folded = true; }
+      }
+      if constexpr (CMAX > 256) {
+        if (!folded && C > 256) { fold(std::integral_constant<int, 8>{}); folded = true; }
+      }
+      if (!folded) {
+        if (C > 128) fold(std::integral_constant<int, 4>{});
+        else if (C > 64) fold(std::integral_constant<int, 2>{});
+        else fold(std::integral_constant<int, 1>{});
+      }
       // strides 32 and 16 by shuffles, 8 .. 1 by DPP row_shl (lane l reads lane l + h of its
       // row); only lanes below the stride keep meaningful sums
       float v = u[0];

@@ -50,19 +50,19 @@ def _run(cmd: list[str]) -> str:
 # every step by that workgroup's runtime. The build refuses such a kernel for the caches, head
 # sizes and query groups of the decode configurations it serves (2-byte K/V, d <= 128, up to 4
 # query heads per KV head); fp32 caches hold twice the row registers and are a parity path.
-_KERNEL = re.compile(r"Function Name: _ZN3ssa13decode_kernelI(\w+?)Li(\d+)ELi(\d+)ELb(\d)ELb(\d)ELb(\d)E")
+_KERNEL = re.compile(r"Function Name: _ZN3ssa13decode_kernelI(\w+?)Li(\d+)ELi(\d+)ELb(\d)ELb(\d)ELb(\d)ELi(\d+)E")
 _OCC = re.compile(r"Occupancy \[waves/SIMD\]: (\d+)")
 
 
 def decode_occupancy(remarks: str) -> dict:
-    """{(dtype, d, GMAX, dense, select, ahead): waves per SIMD} from the compiler's
+    """{(dtype, d, GMAX, dense, select, ahead, slot capacity): waves per SIMD} from the compiler's
     kernel-resource-usage remarks of a decode translation unit."""
     out = {}
     for block in remarks.split("Function Name: ")[1:]:
         m = _KERNEL.match("Function Name: " + block)
         o = _OCC.search(block)
         if m and o:
-            out[(m.group(1), int(m.group(2)), int(m.group(3)), *(int(m.group(i)) for i in (4, 5, 6)))] = int(o.group(1))
+            out[(m.group(1), int(m.group(2)), int(m.group(3)), *(int(m.group(i)) for i in (4, 5, 6, 7)))] = int(o.group(1))
     return out
 
 
