@@ -366,7 +366,7 @@ def main() -> int:
                    "dense_GBs": round(2 * H_KV * N * D * 2 / dense_us / 1e3, 1),
                    "prefill_s": round(sets[-1].prefill_s, 4)},
         "roofline": {"bound": "hbm", "kernel": "ssa_sparse_step with insert-ahead (decode_kernel<bf16,128,2,"
-                               "false,true,true>: selection, attention, merge, next step's insertion)",
+                               "false,true,true,256>: selection, attention, merge, next step's insertion)",
                      "achieved": round(achieved, 1),
                      "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
                      "traffic": _profiled_traffic(),
