@@ -364,6 +364,7 @@ def main() -> int:
         "detail": {**detail, "insert_ahead_us": round(res[("step", HEADLINE)][0] - res[("attn", HEADLINE)][0], 2),
                    "dense_us": round(dense_us, 2),
                    "dense_GBs": round(2 * H_KV * N * D * 2 / dense_us / 1e3, 1),
+                   "dense_frac": round(2 * H_KV * N * D * 2 / dense_us / 1e3 / PEAK_GBS, 4),
                    "prefill_s": round(sets[-1].prefill_s, 4)},
         "roofline": {"bound": "hbm", "kernel": "ssa_sparse_step with insert-ahead (decode_kernel<bf16,128,2,"
                                "false,true,true,256>: selection, attention, merge, next step's insertion)",
@@ -469,7 +470,8 @@ def batched_sweep(args, dev, shapes=None) -> dict:
         time_graph(gd, 3, rot)
         dense_us = min(dense_first, time_graph(gd, reps, rot)[0])
         row.update({"dense_us": round(dense_us, 2), "dense_us_first": round(dense_first, 2),
-                    "dense_GBs": round(kv_bytes / dense_us / 1e3, 1)})
+                    "dense_GBs": round(kv_bytes / dense_us / 1e3, 1),
+                    "dense_frac": round(kv_bytes / dense_us / 1e3 / PEAK_GBS, 4)})
         for b in BATCHED_BUDGETS:
             row[f"{int(b * 100)}%"]["speedup_vs_dense"] = round(dense_us / row[f"{int(b * 100)}%"]["step_us"], 2)
         out[f"{B}x{n}"] = row
