@@ -314,6 +314,24 @@ int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N, int32_t d
 int ssa_linear_swiglu(const void* x, const void* W, void* act, int32_t M, int32_t I, int32_t K, int32_t dtype,
                       void* stream);
 
+/* h [M, N] (the residual stream, updated in place) += x [M, K] W [N, K]^T: ssa_linear_skinny
+ * followed by ssa_rmsnorm_add's add, in one launch with the same bits (the product rounded to
+ * the dtype, then the sum). Same limits as ssa_linear_skinny; h need not be aligned. */
+int ssa_linear_skinny_res(const void* x, const void* W, void* h, int32_t M, int32_t N, int32_t K, int32_t dtype,
+                          void* stream);
+
+/* y [M, N] = (RMSNorm(h) * norm_w) W [N, K]^T for rows h [M, K]: ssa_rmsnorm_add without delta
+ * followed by ssa_linear_skinny, in one launch with the same bits (every workgroup reduces the
+ * rows' squares itself, in ssa_rmsnorm_add's order). Same limits as ssa_linear_skinny; h and
+ * norm_w 16-byte aligned. */
+int ssa_rmsnorm_linear_skinny(const void* h, const void* norm_w, float eps, const void* W, void* y, int32_t M,
+                              int32_t N, int32_t K, int32_t dtype, void* stream);
+
+/* act [M, I] as ssa_linear_swiglu of x = RMSNorm(h) * norm_w for rows h [M, K]: ssa_rmsnorm_add
+ * without delta followed by ssa_linear_swiglu, in one launch with the same bits. */
+int ssa_rmsnorm_linear_swiglu(const void* h, const void* norm_w, float eps, const void* W, void* act, int32_t M,
+                              int32_t I, int32_t K, int32_t dtype, void* stream);
+
 /* h [rows, D] = embed [vocab, D] row tok[r] (int64, clamped to the table), then x = RMSNorm(h) * w
  * as ssa_rmsnorm_add without delta; if n_out, *n_out = *pos + 1 (int32, the step's cache length):
  * the first launch of a decode step. */

@@ -17,9 +17,21 @@
 namespace ssa {
 namespace {
 
+// An fp32 value as computed, for the rounding to the storage dtype that follows: without it the
+// compiler may fold the last multiply into the conversion (v_fma_mix* rounds the exact product
+// once, straight to fp16), which differs from fp32-then-fp16 at fp16 midpoints, so that the same
+// expression could round differently in two kernels.
+__device__ __forceinline__ float f32_done(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
-template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
-template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f32(from_f32<T>(v)); }
+template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(f32_done(v)); }
+template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f32(from_f32<T>(f32_done(v))); }
+
+// The sums of squares of the RMSNorms load each thread's elements in rounds of kRmsU before
+// adding them, in the order of the elements.
+constexpr int kRmsU = 8;
 
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -35,13 +47,25 @@ __global__ __launch_bounds__(256) void rmsnorm_add_kernel(T* __restrict__ h, con
   const int64_t row = (int64_t)blockIdx.x * D;
   const int tid = threadIdx.x;
   float ss = 0.f;
-  for (int i = tid; i < D; i += 256) {
-    float v = ld(h, row + i);
-    if (delta) {
-      v = rnd<T>(v + ld(delta, row + i));
-      st(h, row + i, v);
+  for (int i0 = tid; i0 < D; i0 += 256 * kRmsU) {
+    float v[kRmsU], dv[kRmsU];
+#pragma unroll
+    for (int u = 0; u < kRmsU; ++u) {
+      const int i = min(i0 + 256 * u, D - 1);     // in bounds for every lane: the loads issue together
+      v[u] = ld(h, row + i);
+      dv[u] = delta ? ld(delta, row + i) : 0.f;
     }
-    ss += v * v;
+#pragma unroll
+    for (int u = 0; u < kRmsU; ++u) {
+      const int i = i0 + 256 * u;
+      if (i < D) {
+        if (delta) {
+          v[u] = rnd<T>(v[u] + dv[u]);
+          st(h, row + i, v[u]);
+        }
+        ss += v[u] * v[u];
+      }
+    }
   }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -134,10 +158,15 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu,
 // of 512 elements and dots them with the matching 8 elements of the M rows of x in fp32, then the
 // 64 lane partials are summed by a shuffle tree. Every kernel below uses these two functions, so
 // an output column has the same bits whichever kernel computes it.
-// row(r): the weight row of slot r, or -1 for none (its sums stay 0).
-template <typename T, int MM, int R, typename RowFn>
+// row(r): the weight row of slot r, or -1 for none (its sums are left undefined).
+// NORM: x holds the rows h and the dots take x = round((h * rs[m]) * nw) (nw: the RMSNorm weight),
+// the bits of ssa_rmsnorm_add's output, computed element by element as the chunks are read.
+// pro(): called by every thread once the first round of loads is issued (the NORM path
+// computes rs there, so that its reads are in flight together with the weights').
+template <typename T, int MM, int R, bool NORM, typename RowFn, typename Pro>
 __device__ __forceinline__ void skinny_dots(const T* __restrict__ x, const T* __restrict__ W, int M, int K, int lane,
-                                            RowFn row, float (&acc)[R][MM]) {
+                                            RowFn row, float (&acc)[R][MM], const T* __restrict__ nw,
+                                            const float* rs, Pro pro) {
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -147,30 +176,59 @@ __device__ __forceinline__ void skinny_dots(const T* __restrict__ x, const T* __
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = to_f32(h[e]);
   };
+  // Every load is unconditional, at an in-bounds address (slots without a row read row 0, rows
+  // m >= M read row M - 1, lanes past K read the last chunk), so that a round of loads issues
+  // at once; sums of such slots, rows and lanes are never stored or added.
   int64_t rows[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) rows[r] = row(r);
-#pragma unroll 2
-  for (int k0 = 8 * lane; k0 < K; k0 += 512) {
-    uint4 wq[R], xq[MM];
+  for (int r = 0; r < R; ++r) rows[r] = max(row(r), (int64_t)0);
+  // Chunks of 8 columns at k and k + 512 per round, both loaded before either is used. The
+  // unrolling is written out: the rounding barrier of the NORM path is an asm statement, which
+  // the compiler treats as convergent and does not unroll over a runtime trip count.
+  struct Chunk {
+    uint4 w[R], x[MM], n;
+  };
+  auto load = [&](Chunk& c, int k0) {
+    k0 = min(k0, K - 8);
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      wq[r] = rows[r] >= 0 ? *reinterpret_cast<const uint4*>(W + rows[r] * K + k0) : make_uint4(0, 0, 0, 0);
+    for (int r = 0; r < R; ++r) c.w[r] = *reinterpret_cast<const uint4*>(W + rows[r] * K + k0);
 #pragma unroll
-    for (int m = 0; m < MM; ++m)
-      xq[m] = m < M ? *reinterpret_cast<const uint4*>(x + (int64_t)m * K + k0) : make_uint4(0, 0, 0, 0);
+    for (int m = 0; m < MM; ++m) c.x[m] = *reinterpret_cast<const uint4*>(x + (int64_t)min(m, M - 1) * K + k0);
+    if constexpr (NORM) c.n = *reinterpret_cast<const uint4*>(nw + k0);
+  };
+  auto dots = [&](const Chunk& c) {
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
       float xf[8];
-      widen(xq[m], xf);
+      widen(c.x[m], xf);
+      if constexpr (NORM) {
+        float nf[8];
+        widen(c.n, nf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = rnd<T>((xf[e] * rs[m]) * nf[e]);
+      }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float wf[8];
-        widen(wq[r], wf);
+        widen(c.w[r], wf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][m] = __builtin_fmaf(wf[e], xf[e], acc[r][m]);
       }
     }
+  };
+  Chunk c0, c1;
+  load(c0, 8 * lane);
+  load(c1, 8 * lane + 512);
+  __builtin_amdgcn_sched_barrier(0);        // the weights' loads issue first
+  pro();
+  for (int kb = 0;;) {                      // kb: the round's first column, the same in every lane
+    const int k0 = kb + 8 * lane;
+    if (k0 < K) dots(c0);
+    if (k0 + 512 < K) dots(c1);
+    kb += 1024;
+    if (kb >= K) break;
+    load(c0, kb + 8 * lane);
+    load(c1, kb + 8 * lane + 512);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -182,22 +240,90 @@ __device__ __forceinline__ void skinny_dots(const T* __restrict__ x, const T* __
     }
 }
 
+// 1 / sqrt(mean(h_m^2) + eps) of rows m < M of h [M, D], every thread of the workgroup taking
+// part, in ssa_rmsnorm_add's order: thread t sums elements t, t + 256, ... left to right, then a
+// wave tree, then the four waves in order. load() issues the loads of the first round (kRmsU
+// elements of each row per thread), run() sums them and finishes.
+template <typename T, int MM>
+struct RowNorms {
+  float v[MM][kRmsU];
+  __device__ __forceinline__ void load(const T* __restrict__ h, int M, int D, int i0) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int u = 0; u < kRmsU; ++u) {
+        // in-bounds addresses for every lane, so that the loads issue together
+        const int i = min(i0 + 256 * u, D - 1);
+        v[m][u] = ld(h, (int64_t)min(m, M - 1) * D + i);
+      }
+  }
+  __device__ __forceinline__ void run(const T* __restrict__ h, int M, int D, float eps, float (&rs)[MM]) {
+    __shared__ float red[MM][4];
+    const int tid = threadIdx.x;
+    float ss[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) ss[m] = 0.f;
+    // b: the round's first element, the same in every thread. Every loaded value is used, so
+    // that no load is moved behind a branch: rows m >= M sum copies of row M - 1 (not used), and
+    // elements past D add +0, which leaves a sum of squares unchanged.
+    auto add = [&](int b) {
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int u = 0; u < kRmsU; ++u) ss[m] += b + tid + 256 * u < D ? v[m][u] * v[m][u] : 0.f;
+    };
+    // the first round outside the loop: waits inside a loop would be sized for the loop's own
+    // loads and so also cover every load still in flight when it is entered
+    add(0);
+    for (int b = 256 * kRmsU; b < D; b += 256 * kRmsU) {
+      load(h, M, D, b + tid);
+      add(b);
+    }
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      if (m < M) {
+        const float t = wave_sum(ss[m]);
+        if ((tid & 63) == 0) red[m][tid >> 6] = t;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      rs[m] = m < M ? 1.0f / sqrtf((red[m][0] + red[m][1] + red[m][2] + red[m][3]) / (float)D + eps) : 0.f;
+  }
+};
+
 // y [M, N] = x [M, K] . W[N, K]^T, rounded once to the output dtype. Wave w of workgroup b owns
 // output columns n0 = (4 b + w) R .. n0 + R.
-template <typename T, int MM, int R>
+// NORM: x holds rows h and the product is taken of rmsnorm(h) * nw (ssa_rmsnorm_add's bits).
+// RES: y is the residual stream, y += round(product), rounded as ssa_rmsnorm_add's add.
+template <typename T, int MM, int R, bool NORM = false, bool RES = false>
 __global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, const T* __restrict__ W,
-                                                     T* __restrict__ y, int M, int N, int K) {
+                                                     T* __restrict__ y, int M, int N, int K,
+                                                     const T* __restrict__ nw = nullptr, float eps = 0.f) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * R;
-  if (n0 >= N) return;
-  float acc[R][MM];
-  skinny_dots<T, MM, R>(x, W, M, K, lane, [&](int r) { return n0 + r < N ? (int64_t)(n0 + r) : (int64_t)-1; }, acc);
+  if (!NORM && n0 >= N) return;     // with NORM every wave takes part in the row norms
+  float rs[MM], acc[R][MM];
+  RowNorms<T, MM> norms;
+  skinny_dots<T, MM, R, NORM>(
+      x, W, M, K, lane, [&](int r) { return n0 + r < N ? (int64_t)(n0 + r) : (int64_t)-1; }, acc, nw, rs,
+      [&] {
+        if constexpr (NORM) {
+          norms.load(x, M, K, threadIdx.x);
+          norms.run(x, M, K, eps, rs);
+        }
+      });
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < MM; ++m)
-        if (m < M && n0 + r < N) st(y, (int64_t)m * N + n0 + r, acc[r][m]);
+        if (m < M && n0 + r < N) {
+          const int64_t o = (int64_t)m * N + n0 + r;
+          if constexpr (RES) st(y, o, ld(y, o) + rnd<T>(acc[r][m]));
+          else st(y, o, acc[r][m]);
+        }
   }
 }
 
@@ -205,17 +331,29 @@ __global__ __launch_bounds__(256) void skinny_kernel(const T* __restrict__ x, co
 // first, then up rows): the gate/up projection with the SwiGLU activation as its epilogue, equal
 // bit for bit to ssa_linear_skinny followed by ssa_silu_mul. Wave w of workgroup b owns
 // activation columns c0 = 2 (4 b + w), c0 + 1: weight rows c0, c0 + 1, I + c0, I + c0 + 1.
-template <typename T, int MM>
+// NORM: x holds rows h and the product is taken of rmsnorm(h) * nw (ssa_rmsnorm_add's bits).
+template <typename T, int MM, bool NORM = false>
 __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ x, const T* __restrict__ W,
-                                                     T* __restrict__ act, int M, int I, int K) {
+                                                     T* __restrict__ act, int M, int I, int K,
+                                                     const T* __restrict__ nw = nullptr, float eps = 0.f) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c0 = (blockIdx.x * 4 + wave) * 2;
-  if (c0 >= I) return;
-  float acc[4][MM];
-  skinny_dots<T, MM, 4>(x, W, M, K, lane, [&](int r) {
-    const int c = c0 + (r & 1);
-    return c < I ? (int64_t)((r < 2 ? 0 : I) + c) : (int64_t)-1;
-  }, acc);
+  if (!NORM && c0 >= I) return;     // with NORM every wave takes part in the row norms
+  float rs[MM], acc[4][MM];
+  RowNorms<T, MM> norms;
+  skinny_dots<T, MM, 4, NORM>(
+      x, W, M, K, lane,
+      [&](int r) {
+        const int c = c0 + (r & 1);
+        return c < I ? (int64_t)((r < 2 ? 0 : I) + c) : (int64_t)-1;
+      },
+      acc, nw, rs,
+      [&] {
+        if constexpr (NORM) {
+          norms.load(x, M, K, threadIdx.x);
+          norms.run(x, M, K, eps, rs);
+        }
+      });
   if (lane == 0) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
@@ -315,18 +453,22 @@ extern "C" int ssa_silu_mul(const void* gu, void* out, int32_t rows, int32_t I, 
   });
 }
 
-extern "C" int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
-                                 void* stream) {
-  if (!x || !W || !y || M < 1 || M > 8 || N < 1 || K < 8 || K % 8) return hipErrorInvalidValue;
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) return hipErrorInvalidValue;
+namespace {
+
+template <bool NORM, bool RES>
+int launch_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
+                  const void* nw, float eps, void* stream) {
+  if (!x || !W || !y || M < 1 || M > 8 || N < 1 || K < 8 || K % 8 || (NORM && !nw)) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(nw)) & 15)
+    return hipErrorInvalidValue;
   if (dtype != kBF16 && dtype != kF16) return hipErrorInvalidValue;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto go = [&](auto tag, auto mm, auto rr) {
     using T = decltype(tag);
     constexpr int MM = decltype(mm)::value, R = decltype(rr)::value;
     const int grid = (N + 4 * R - 1) / (4 * R);
-    hipLaunchKernelGGL((skinny_kernel<T, MM, R>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x),
-                       static_cast<const T*>(W), static_cast<T*>(y), M, N, K);
+    hipLaunchKernelGGL((skinny_kernel<T, MM, R, NORM, RES>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x),
+                       static_cast<const T*>(W), static_cast<T*>(y), M, N, K, static_cast<const T*>(nw), eps);
     return (int)hipGetLastError();
   };
   // rows per wave: 4 when the columns give at least 1024 waves, else 1
@@ -341,6 +483,48 @@ extern "C" int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t 
     return pick(tag, std::integral_constant<int, 8>{});
   };
   return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
+}
+
+template <bool NORM>
+int launch_swiglu(const void* x, const void* W, void* act, int32_t M, int32_t I, int32_t K, int32_t dtype,
+                  const void* nw, float eps, void* stream) {
+  if (!x || !W || !act || M < 1 || M > 8 || I < 1 || K < 8 || K % 8 || (NORM && !nw)) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(nw)) & 15)
+    return hipErrorInvalidValue;
+  if (dtype != kBF16 && dtype != kF16) return hipErrorInvalidValue;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto go = [&](auto tag, auto mm) {
+    using T = decltype(tag);
+    constexpr int MM = decltype(mm)::value;
+    const int grid = (I + 7) / 8;
+    hipLaunchKernelGGL((swiglu_kernel<T, MM, NORM>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x),
+                       static_cast<const T*>(W), static_cast<T*>(act), M, I, K, static_cast<const T*>(nw), eps);
+    return (int)hipGetLastError();
+  };
+  auto bym = [&](auto tag) {
+    if (M <= 1) return go(tag, std::integral_constant<int, 1>{});
+    if (M <= 2) return go(tag, std::integral_constant<int, 2>{});
+    if (M <= 4) return go(tag, std::integral_constant<int, 4>{});
+    return go(tag, std::integral_constant<int, 8>{});
+  };
+  return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
+}
+
+}  // namespace
+
+extern "C" int ssa_linear_skinny(const void* x, const void* W, void* y, int32_t M, int32_t N, int32_t K, int32_t dtype,
+                                 void* stream) {
+  return launch_skinny<false, false>(x, W, y, M, N, K, dtype, nullptr, 0.f, stream);
+}
+
+extern "C" int ssa_linear_skinny_res(const void* x, const void* W, void* h, int32_t M, int32_t N, int32_t K,
+                                     int32_t dtype, void* stream) {
+  return launch_skinny<false, true>(x, W, h, M, N, K, dtype, nullptr, 0.f, stream);
+}
+
+extern "C" int ssa_rmsnorm_linear_skinny(const void* h, const void* norm_w, float eps, const void* W, void* y,
+                                         int32_t M, int32_t N, int32_t K, int32_t dtype, void* stream) {
+  return launch_skinny<true, false>(h, W, y, M, N, K, dtype, norm_w, eps, stream);
 }
 
 // out [M] int64 = argmax over each row of x [M, N]: the first index of the maximum, a NaN counting
@@ -451,25 +635,12 @@ extern "C" int ssa_argmax_rows(const void* x, int64_t* out, int32_t M, int32_t N
 
 extern "C" int ssa_linear_swiglu(const void* x, const void* W, void* act, int32_t M, int32_t I, int32_t K,
                                  int32_t dtype, void* stream) {
-  if (!x || !W || !act || M < 1 || M > 8 || I < 1 || K < 8 || K % 8) return hipErrorInvalidValue;
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) return hipErrorInvalidValue;
-  if (dtype != kBF16 && dtype != kF16) return hipErrorInvalidValue;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  auto go = [&](auto tag, auto mm) {
-    using T = decltype(tag);
-    constexpr int MM = decltype(mm)::value;
-    const int grid = (I + 7) / 8;
-    hipLaunchKernelGGL((swiglu_kernel<T, MM>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x),
-                       static_cast<const T*>(W), static_cast<T*>(act), M, I, K);
-    return (int)hipGetLastError();
-  };
-  auto bym = [&](auto tag) {
-    if (M <= 1) return go(tag, std::integral_constant<int, 1>{});
-    if (M <= 2) return go(tag, std::integral_constant<int, 2>{});
-    if (M <= 4) return go(tag, std::integral_constant<int, 4>{});
-    return go(tag, std::integral_constant<int, 8>{});
-  };
-  return dtype == kBF16 ? bym(__hip_bfloat16{}) : bym(__half{});
+  return launch_swiglu<false>(x, W, act, M, I, K, dtype, nullptr, 0.f, stream);
+}
+
+extern "C" int ssa_rmsnorm_linear_swiglu(const void* h, const void* norm_w, float eps, const void* W, void* act,
+                                         int32_t M, int32_t I, int32_t K, int32_t dtype, void* stream) {
+  return launch_swiglu<true>(h, W, act, M, I, K, dtype, norm_w, eps, stream);
 }
 
 extern "C" int ssa_embed_rmsnorm(const int64_t* tok, const void* embed, void* h, const void* w, void* x, int32_t rows,

@@ -141,6 +141,11 @@ ENTRY_POINTS = {
     "ssa_linear_skinny": (ct.c_int, [vp, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
     "ssa_argmax_rows": (ct.c_int, [vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, vp, vp]),
     "ssa_linear_swiglu": (ct.c_int, [vp, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
+    "ssa_linear_skinny_res": (ct.c_int, [vp, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32, ct.c_int32, vp]),
+    "ssa_rmsnorm_linear_skinny": (ct.c_int, [vp, vp, ct.c_float, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32,
+                                             ct.c_int32, vp]),
+    "ssa_rmsnorm_linear_swiglu": (ct.c_int, [vp, vp, ct.c_float, vp, vp, ct.c_int32, ct.c_int32, ct.c_int32,
+                                             ct.c_int32, vp]),
     "ssa_embed_rmsnorm": (ct.c_int, [vp, vp, vp, vp, vp, ct.c_int32, ct.c_int32, i64, ct.c_float, vp, vp, ct.c_int32,
                                      vp]),
 }

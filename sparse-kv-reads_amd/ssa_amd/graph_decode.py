@@ -90,14 +90,22 @@ class GraphDecoder:
             raise ValueError(f"unknown glue {glue!r}")
         self.glue = glue
         # "fused" folds SwiGLU into the gate/up projection where the kernel allows it (2-byte
-        # weights, batch <= 8); "split" runs the two ops as two launches (the same bits)
+        # weights, batch <= 8), and the residual adds and RMSNorms into the projections either
+        # side of them (the add into the o and down projections' epilogues, each norm into the
+        # next projection's prologue), which leaves five launches per layer besides the attention;
+        # "split" runs every op as its own launch. Both give the same bits.
         self._merge_gu = (glue == "fused" and dtype in (torch.bfloat16, torch.float16) and B <= 8
                           and cfg.hidden_size % 8 == 0)
+        self._fuse_norm = self._merge_gu and cfg.intermediate_size % 8 == 0 and (self.H * self.d) % 8 == 0
         if glue != "torch":
             with torch.no_grad():
                 self._wqkv = [torch.cat((l.attn.q.weight, l.attn.k.weight, l.attn.v.weight)) for l in model.layers]
                 self._wgu = [torch.cat((l.ffn.gate.weight, l.ffn.up.weight)) for l in model.layers]
             self._h = torch.empty(B, cfg.hidden_size, device=dev, dtype=dtype)     # the residual stream
+            if self._fuse_norm:            # the projections' outputs, reused by every layer and step
+                head = model.embed.weight if model.lm_head is None else model.lm_head.weight
+                self._qkv = torch.empty(B, self._wqkv[0].shape[0], device=dev, dtype=dtype)
+                self._logits = torch.empty(B, head.shape[0], device=dev, dtype=dtype)
             self._x = torch.empty(B, cfg.hidden_size, device=dev, dtype=dtype)
             self._qh = torch.empty(B * self.H, self.d, device=dev, dtype=dtype)
             self._act = torch.empty(B, cfg.intermediate_size, device=dev, dtype=dtype)
@@ -150,6 +158,8 @@ class GraphDecoder:
                                       eps, self.pos.data_ptr(), self.n_dev.data_ptr(), dt, s), "ssa_embed_rmsnorm")
         if self.insert_all is not None:
             self.insert_all(self.n_dev)
+        if self._fuse_norm:
+            return self._body_fused_norm()
         for i, layer in enumerate(m.layers):
             a, f = layer.attn, layer.ffn
             kc, vc = self.cache.k[i], self.cache.v[i]
@@ -177,6 +187,40 @@ class GraphDecoder:
         if self.greedy:
             check(lib().ssa_argmax_rows(logits.data_ptr(), self.next_tok.data_ptr(), B, logits.shape[1], dt,
                                         self._argmax_work.data_ptr(), s), "ssa_argmax_rows")
+        return logits.view(B, 1, -1)
+
+    def _body_fused_norm(self) -> torch.Tensor:
+        """The layers after the embedding with the residual adds and RMSNorms inside the
+        projections: per layer rmsnorm + qkv, q/k norm + rotary + cache write, attention,
+        o projection + residual add, rmsnorm + gate/up + SwiGLU, down projection + residual add."""
+        m, H, H_kv, d, B = self.model, self.H, self.H_kv, self.d, self.B
+        s, h, eps, dt = stream_ptr(self.tok.device), self._h, self._eps, self._dt
+        act, I, D = self._act, self._act.shape[1], h.shape[1]
+        L = lib()
+        for i, layer in enumerate(m.layers):
+            a, f = layer.attn, layer.ffn
+            kc, vc = self.cache.k[i], self.cache.v[i]
+            qkv = self._qkv
+            check(L.ssa_rmsnorm_linear_skinny(h.data_ptr(), layer.norm1.weight.data_ptr(), eps, self._wqkv[i].data_ptr(),
+                                              qkv.data_ptr(), B, qkv.shape[1], D, dt, s), "ssa_rmsnorm_linear_skinny")
+            check(L.ssa_qk_norm_rope_cache(qkv.data_ptr(), a.q_norm.weight.data_ptr(), a.k_norm.weight.data_ptr(),
+                                           m.rope_cos.data_ptr(), m.rope_sin.data_ptr(), self.pos.data_ptr(),
+                                           self._qh.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0),
+                                           kc.stride(1), kc.stride(2), B, H, H_kv, d, eps, dt, s), "ssa_qk_norm_rope_cache")
+            out = self._attend(i, self._qh, kc, vc)
+            check(L.ssa_linear_skinny_res(out.data_ptr(), a.o.weight.data_ptr(), h.data_ptr(), B, D, H * d, dt, s),
+                  "ssa_linear_skinny_res")
+            check(L.ssa_rmsnorm_linear_swiglu(h.data_ptr(), layer.norm2.weight.data_ptr(), eps, self._wgu[i].data_ptr(),
+                                              act.data_ptr(), B, I, D, dt, s), "ssa_rmsnorm_linear_swiglu")
+            check(L.ssa_linear_skinny_res(act.data_ptr(), f.down.weight.data_ptr(), h.data_ptr(), B, D, I, dt, s),
+                  "ssa_linear_skinny_res")
+        head = m.embed.weight if m.lm_head is None else m.lm_head.weight
+        logits = self._logits
+        check(L.ssa_rmsnorm_linear_skinny(h.data_ptr(), m.final_norm.weight.data_ptr(), eps, head.data_ptr(),
+                                          logits.data_ptr(), B, head.shape[0], D, dt, s), "ssa_rmsnorm_linear_skinny")
+        if self.greedy:
+            check(L.ssa_argmax_rows(logits.data_ptr(), self.next_tok.data_ptr(), B, logits.shape[1], dt,
+                                    self._argmax_work.data_ptr(), s), "ssa_argmax_rows")
         return logits.view(B, 1, -1)
 
     def _body(self) -> torch.Tensor:

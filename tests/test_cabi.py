@@ -81,6 +81,10 @@ def test_glue_entry_points_refuse_bad_arguments_before_any_launch():
     assert h.ssa_linear_swiglu(fake, fake, fake, 2, 64, 60, 1, None) != 0      # K not a multiple of 8
     assert h.ssa_linear_swiglu(fake, fake, fake, 2, 64, 64, 0, None) != 0      # fp32 weights
     assert h.ssa_linear_skinny(fake, fake, fake, 0, 64, 64, 1, None) != 0
+    assert h.ssa_linear_skinny_res(fake, fake, fake, 9, 64, 64, 1, None) != 0          # batch above 8
+    assert h.ssa_rmsnorm_linear_skinny(fake, None, 1e-6, fake, fake, 2, 64, 64, 1, None) != 0   # no norm weight
+    assert h.ssa_rmsnorm_linear_skinny(fake, fake + 8, 1e-6, fake, fake, 2, 64, 64, 1, None) != 0  # misaligned
+    assert h.ssa_rmsnorm_linear_swiglu(fake, fake, 1e-6, fake, fake, 2, 64, 60, 1, None) != 0   # K not a multiple of 8
     assert h.ssa_argmax_rows(fake, fake, 2, 100, 1, None, None) != 0           # no work buffer
     assert h.ssa_argmax_rows(fake, fake, 0, 100, 1, fake, None) != 0
     assert h.ssa_embed_rmsnorm(None, fake, fake, fake, fake, 2, 64, 10, 1e-6, fake, fake, 1, None) != 0

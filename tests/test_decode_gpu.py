@@ -260,3 +260,45 @@ def test_argmax_rows_is_torch_argmax(N, dtype):
     z[0, 3] = -0.0                                      # -0 and +0 are equal: the first index wins
     check(L.ssa_argmax_rows(z.data_ptr(), out.data_ptr(), 1, N, dtype_tag(dtype), work.data_ptr(), s), "argmax")
     assert int(out[0]) == 0
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 6144, 2560), (2, 1024, 1024), (3, 333, 264), (8, 4096, 2048)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_norm_and_residual_inside_the_projections_keep_the_bits(M, N, K, dtype):
+    """ssa_rmsnorm_linear_skinny / ssa_rmsnorm_linear_swiglu (the RMSNorm computed in the
+    projection's prologue) and ssa_linear_skinny_res (the residual add in its epilogue) against
+    the launches they replace, ssa_rmsnorm_add then ssa_linear_skinny / ssa_linear_swiglu, and
+    ssa_linear_skinny then ssa_rmsnorm_add's add: the same bits."""
+    check, dtype_tag, L, s = _lib()
+    dt = dtype_tag(dtype)
+    g = torch.Generator(device="cuda").manual_seed(M * 13 + N)
+    h = (torch.randn(M, K, device="cuda", generator=g) * 3).to(dtype)
+    nw = (1 + 0.1 * torch.randn(K, device="cuda", generator=g)).to(dtype)
+    W = (torch.randn(N, K, device="cuda", generator=g) * 0.05).to(dtype)
+    Wg = (torch.randn(2 * N, K, device="cuda", generator=g) * 0.05).to(dtype)
+    # rmsnorm + projection
+    x = torch.empty_like(h)
+    check(L.ssa_rmsnorm_add(h.data_ptr(), None, nw.data_ptr(), x.data_ptr(), M, K, 1e-6, dt, s), "rmsnorm_add")
+    want = torch.empty(M, N, device="cuda", dtype=dtype)
+    check(L.ssa_linear_skinny(x.data_ptr(), W.data_ptr(), want.data_ptr(), M, N, K, dt, s), "skinny")
+    got = torch.full((M, N), float("nan"), device="cuda", dtype=dtype)
+    check(L.ssa_rmsnorm_linear_skinny(h.data_ptr(), nw.data_ptr(), 1e-6, W.data_ptr(), got.data_ptr(), M, N, K, dt, s),
+          "rmsnorm_linear_skinny")
+    assert torch.equal(got, want)
+    # rmsnorm + gate/up + SwiGLU
+    want = torch.empty(M, N, device="cuda", dtype=dtype)
+    check(L.ssa_linear_swiglu(x.data_ptr(), Wg.data_ptr(), want.data_ptr(), M, N, K, dt, s), "swiglu")
+    got = torch.full((M, N), float("nan"), device="cuda", dtype=dtype)
+    check(L.ssa_rmsnorm_linear_swiglu(h.data_ptr(), nw.data_ptr(), 1e-6, Wg.data_ptr(), got.data_ptr(), M, N, K, dt, s),
+          "rmsnorm_linear_swiglu")
+    assert torch.equal(got, want)
+    # projection + residual add: h2 [M, N] += x W^T
+    h2 = (torch.randn(M, N, device="cuda", generator=g) * 3).to(dtype)
+    want_h = h2.clone()
+    y = torch.empty(M, N, device="cuda", dtype=dtype)
+    check(L.ssa_linear_skinny(x.data_ptr(), W.data_ptr(), y.data_ptr(), M, N, K, dt, s), "skinny")
+    scratch = torch.empty_like(want_h)
+    check(L.ssa_rmsnorm_add(want_h.data_ptr(), y.data_ptr(), torch.ones(N, device="cuda", dtype=dtype).data_ptr(),
+                            scratch.data_ptr(), M, N, 1e-6, dt, s), "rmsnorm_add")
+    check(L.ssa_linear_skinny_res(x.data_ptr(), W.data_ptr(), h2.data_ptr(), M, N, K, dt, s), "skinny_res")
+    assert torch.equal(h2, want_h)
