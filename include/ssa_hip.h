@@ -151,7 +151,9 @@ int ssa_select(const ssa_index_state_t* st, const ssa_insert_args_t* ins, const 
  * window at length n + 1 (ins_ahead's n fields are ignored), splits included: the state is then
  * what ssa_insert would make of it at the start of the next step, so a decode loop that grows n
  * by one per step needs no insertion launch. The keys at positions < n + 1 - window must be in
- * the cache.
+ * the cache. The insertion is staged by one extra workgroup per head while Hk x (S + 1)
+ * workgroups fit two per compute unit, otherwise by each head's split S - 1 after its attention
+ * (no extra workgroups); either way the state and outputs are the same.
  * Replaces the per-layer bin + score + pick + compact + list + merge launches of
  * SphereIndexGraph.step (src/ssa/kernels/graph_kernels.py:220-244). */
 int ssa_sparse_step(const ssa_index_state_t* st, const ssa_select_args_t* sel, const ssa_attn_args_t* args,

@@ -1,6 +1,7 @@
 // C ABI of the attention entry points, and the standalone merge and compaction kernels of the
 // reference's functional API. The decode kernel itself is in decode.h, instantiated once per KV
 // dtype by decode_bf16.hip, decode_f16.hip and decode_f32.hip.
+#include <atomic>
 #include <mutex>
 
 #include "decode.h"
@@ -130,6 +131,17 @@ bool rows_aligned(const ssa_attn_args_t* x) {
          s16(x->s_kn, ke) && s16(x->s_vh, ke) && s16(x->s_vn, ke) && (x->d * ke) % 16 == 0;
 }
 
+// Compute units of the current device (0 if unknown), looked up once per device.
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int c = cus[dev].load(std::memory_order_relaxed);
+  if (c == 0 && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+    cus[dev].store(c, std::memory_order_relaxed);
+  return c > 0 ? c : 0;
+}
+
 // zero_first: arrival counters to clear (a fill kernel on the same stream) once the arguments
 // have been checked and before the decode kernel is launched; nullptr for none.
 int launch_decode(const ssa_attn_args_t* x, int mode, void* stream, const ssa_index_state_t* st = nullptr,
@@ -173,6 +185,11 @@ int launch_decode(const ssa_attn_args_t* x, int mode, void* stream, const ssa_in
         return hipErrorInvalidValue;
       p.ins = *ins;
       mode = kFusedAhead;
+      // An extra stager workgroup per head while heads x (S + 1) workgroups are all resident
+      // (two per compute unit); past that, split S - 1 stages after its attention, which costs
+      // less than a second round of workgroups. Both leave the same state.
+      const int cus = device_cus();
+      p.fold_stage = cus > 0 && (int64_t)x->n_heads * (x->S + 1) > 2 * (int64_t)cus;
     }
   }
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);

@@ -48,8 +48,10 @@ struct DecodeParams {
   ssa_index_state_t st;
   double budget; int group; float sel_scale;
   // insertion ahead (fused mode with AHEAD): after the merge, the last workgroup of each head
-  // bins the keys that leave the window at length n + 1
+  // bins the keys that leave the window at length n + 1, as staged by an extra workgroup per
+  // head or, with fold_stage (when the extra workgroups would not all be resident), by split S - 1
   ssa_insert_args_t ins;
+  int fold_stage;
 };
 
 constexpr int kThreads = 256;
@@ -192,15 +194,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
   const int s1 = min(s0 + chunk, n);
   auto block_pos = [&](int it, int u) { return (sp + S * (PER * it + u)) * kThreads; };
   const int16_t* labrow = DENSE ? nullptr : a.labels + (int64_t)h * a.s_lh;
-  // AHEAD: workgroup S of each head (one past the splits) stages the next step's insertion
-  const bool stager = AHEAD && sp == S;
-  if (stager) {
-    InsPre<AHEAD ? D : 16> spre;
-    if constexpr (AHEAD) {
-      insert_prefetch<D>(spre, a.st, a.ins, h, n + 1);
-      insert_stage<D>(sm.u.tail, a.st, a.ins, h, spre, n + 1);
-    }
-  } else {
+  // AHEAD: the next step's insertion is staged by workgroup S of each head (one past the splits)
+  // or, with fold_stage, by split S - 1 once its own attention is done
+  const bool stager = AHEAD && !a.fold_stage && sp == S;
+  if (!stager) {
     // Issue the selection state's and the first page's label loads before anything waits on memory.
     int n_act = 0, end_h = 0;
     uint32_t touch = 0;
@@ -479,11 +476,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     }
     if (tid == 0) __hip_atomic_store(a.part_cnt + pidx, rows_read, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }  // attention workgroups
+  if constexpr (AHEAD) {
+    if (stager || (a.fold_stage && sp == S - 1)) {
+      if (!stager) __syncthreads();    // the attention is done with sm.u
+      InsPre<D> spre;
+      insert_prefetch<D>(spre, a.st, a.ins, h, n + 1);
+      insert_stage<D>(sm.u.tail, a.st, a.ins, h, spre, n + 1);
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);       // this thread's stores have reached the coherence point
   __syncthreads();
   if (tid == 0) {
     const int old = __hip_atomic_fetch_add(a.counter + h, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm.last = (old == S - 1 + (AHEAD ? 1 : 0));
+    sm.last = (old == S - 1 + (AHEAD && !a.fold_stage ? 1 : 0));
   }
   __syncthreads();
   if (!sm.last) return;
@@ -625,7 +630,7 @@ enum Mode { kDense = 0, kLabelled = 1, kFused = 2, kFusedAhead = 3 };
 // per-slot registers, LDS and code then cover 256 slots instead of 1024.
 template <typename T, int D, int GMAX>
 hipError_t launch_decode_t(const DecodeParams& p, int mode, hipStream_t st) {
-  dim3 grid(p.S + (mode == kFusedAhead ? 1 : 0), p.n_heads);
+  dim3 grid(p.S + (mode == kFusedAhead && !p.fold_stage ? 1 : 0), p.n_heads);
   const bool small = D == 128 && p.st.C <= 256;
   if (mode == kDense) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, true>), grid, dim3(kThreads), 0, st, p);
   else if (mode == kLabelled) hipLaunchKernelGGL((decode_kernel<T, D, GMAX, false>), grid, dim3(kThreads), 0, st, p);

@@ -10,20 +10,25 @@ tokens, so it is captured once and replayed with a single graph launch per token
 Batching: the cache ``[B, H_kv, L, d]`` is viewed as ``[B·H_kv, L, d]`` and the queries
 ``[B, H, d]`` as ``[B·H, d]`` (every (sequence, KV head) is independent), without copying.
 
-Insertion: with insert-ahead (``SphereIndexGraph.insert_ahead``, chosen per layer at
-``prepare``) each layer's step launch bins its next key; otherwise one ``AllLayerInsert`` launch
-bins every layer's key at the start of the step, as the reference's ``fused_insert`` does.
+Insertion: with insert-ahead each layer's step launch bins its next key. It is used while the
+step's extra stager workgroups (one per head) fit beside the splits, or when asked for with
+``insert_ahead=True``; otherwise one ``AllLayerInsert`` launch bins every layer's key at the start
+of the step, as the reference's ``fused_insert`` does.
 
-Glue: with ``glue="fused"`` (the default) a layer is six launches besides the attention step:
-the q/k/v projection, ``ssa_qk_norm_rope_cache`` (q/k RMSNorm, rotary embedding, KV-cache write),
-the o projection, ``ssa_rmsnorm_add`` (residual add + RMSNorm), ``ssa_linear_swiglu`` (the
-gate/up projection with SwiGLU as its epilogue), the down projection and ``ssa_rmsnorm_add``; the
-projections are weight-streaming kernels for the decode batch (``ssa_linear_skinny``), the step
-opens with ``ssa_embed_rmsnorm`` and, with ``greedy``, ends with ``ssa_argmax_rows``.
-``glue="split"`` runs the gate/up projection and SwiGLU as two launches (the same bits), and
-``glue="torch"`` the ~60 element-wise launches of the model's own modules per layer, as the
-reference's ``_body`` runs them. At batch 1-2 every dependent launch costs a few microseconds
-whatever its size, so the launch count is what the glue is designed around.
+Glue: with ``glue="fused"`` (the default) a layer is five launches besides the attention step:
+``ssa_rmsnorm_linear_skinny`` (the input RMSNorm and the q/k/v projection),
+``ssa_qk_norm_rope_cache`` (q/k RMSNorm, rotary embedding, KV-cache write),
+``ssa_linear_skinny_res`` (the o projection added into the residual stream),
+``ssa_rmsnorm_linear_swiglu`` (the post-attention RMSNorm, the gate/up projection and SwiGLU)
+and ``ssa_linear_skinny_res`` (the down projection); the projections are weight-streaming
+kernels for the decode batch, the step opens with ``ssa_embed_rmsnorm``, the final RMSNorm rides
+in the LM head's projection and, with ``greedy``, ``ssa_argmax_rows`` ends the step. Where those
+kernels do not apply (batch above 8, fp32 weights, widths not a multiple of 8) the norms and adds
+run as ``ssa_rmsnorm_add`` and the projections as ``ssa_linear_skinny`` / ``ssa_linear_swiglu``.
+``glue="split"`` runs every op as its own launch (the same bits), and ``glue="torch"`` the ~60
+element-wise launches of the model's own modules per layer, as the reference's ``_body`` runs
+them. At batch 1-2 every dependent launch costs a few microseconds whatever its size, so the
+launch count is what the glue is designed around.
 """
 
 from __future__ import annotations
@@ -85,6 +90,7 @@ class GraphDecoder:
         self.next_tok = torch.zeros(B, 1, dtype=torch.long, device=dev)   # with greedy: argmax of the logits
         self._argmax_work = torch.zeros(2 * B, dtype=torch.long, device=dev)  # ssa_argmax_rows' key + count
         self.fused_insert = fused_insert and mode == "cluster" and window >= 1
+        self._ahead_forced = insert_ahead is True   # else every layer's keys in one launch past the stagers
         self.insert_all = None
         if glue not in ("fused", "split", "torch"):
             raise ValueError(f"unknown glue {glue!r}")
@@ -122,7 +128,8 @@ class GraphDecoder:
             return
         for i, idx in enumerate(self.attn):
             idx.prepare(self._heads(self.cache.k[i]), n, self.B * self.H)
-        if self.fused_insert and not all(idx.insert_ahead for idx in self.attn):
+        if self.fused_insert and not all(idx.insert_ahead and (idx.extra_stagers_fit() or self._ahead_forced)
+                                         for idx in self.attn):
             for idx in self.attn:                       # one insertion launch for every layer
                 idx.insert_ahead = False
             self.insert_all = AllLayerInsert(self.attn, [self._heads(k) for k in self.cache.k[:len(self.attn)]])

@@ -116,11 +116,16 @@ class SphereIndexGraph(SphereIndexFused):
         self.out = torch.empty(H, d, device=dev, dtype=K.dtype)
 
     def auto_insert_ahead(self) -> bool:
-        """Bin the next step's key inside the fused launch (one extra workgroup per head) while
-        the heads are few, where the step is latency-bound and a second launch costs more than
-        the extra workgroups; with many heads the extra workgroups compete with the row loads
-        and a separate insertion launch is cheaper (measured on MI355X: batch 8 x 8k and
-        2 x 32k gain 5-9 us per step, batch 16 x 32k and 64 x 32k lose 19-240 us)."""
+        """Bin the next step's key inside the fused launch. The library stages it in one extra
+        workgroup per head while those fit beside the splits (two workgroups per compute unit),
+        else in each head's last split after its attention; either beats a separate insertion
+        launch (measured on MI355X: batch 8 x 8k and 2 x 32k gain 5-9 us per step, 16 x 32k
+        6-8 us, 64 x 32k -1..+4 us)."""
+        return True
+
+    def extra_stagers_fit(self) -> bool:
+        """Whether the fused launch's extra stager workgroups (one per head) fit beside the
+        splits; past that a model's decode loop bins every layer's keys in one launch."""
         return 4 * self.H_kv <= cu_count(self.device)
 
     def _init(self, K, n):

@@ -28,10 +28,10 @@ def _cache(H_kv, n, *, H, seed, centers=16):
     return K[0], V[0], q[0].contiguous()
 
 
-def _graph_index(ahead, K, n0, H, cap, budget):
+def _graph_index(ahead, K, n0, H, cap, budget, splits=None):
     from ssa_amd.graph_kernels import SphereIndexGraph
     idx = SphereIndexGraph(budget=budget, insert_ahead=ahead, C=128, C_init=16, window=16, delta=math.inf,
-                           capacity=K.shape[1], check_every=10 ** 9, partition="kmeans")
+                           capacity=K.shape[1], check_every=10 ** 9, partition="kmeans", num_splits=splits)
     idx.observe(K, n0)
     idx.cap.fill_(cap)                        # split under the cap from the first inserted key on
     idx.prepare(K, n0, H)
@@ -48,14 +48,20 @@ def _same_state(a, b):
         assert torch.equal(x, y), f
 
 
+# (KV heads, splits): 3 heads stage in an extra workgroup per head; 128 x 4 and 67 x 8 give more
+# than two workgroups per compute unit with one, so split S - 1 of each head stages instead
+@pytest.mark.parametrize("H_kv,splits,steps", [(3, None, 120), (128, 4, 40), (67, 8, 40)])
 @pytest.mark.parametrize("budget", [0.05, 0.2])
-def test_insert_ahead_matches_insertion_at_step_start(budget):
+def test_insert_ahead_matches_insertion_at_step_start(budget, H_kv, splits, steps):
     from ssa_amd._lib import check, lib, stream_ptr
-    H_kv, H, n0, steps = 3, 6, 1000, 120
+    from ssa_amd.labeled_attn import cu_count
+    H, n0 = 2 * H_kv, 1000
+    if splits is not None:
+        assert H_kv * (splits + 1) > 2 * cu_count("cuda"), "the case should fold the staging"
     K, V, q = _cache(H_kv, n0 + steps + 8, H=H, seed=11)
     cap = float(1.5 * (n0 - 17) / 16)
-    a = _graph_index(True, K, n0, H, cap, budget)
-    b = _graph_index(False, K, n0, H, cap, budget)
+    a = _graph_index(True, K, n0, H, cap, budget, splits)
+    b = _graph_index(False, K, n0, H, cap, budget, splits)
     n_a = torch.full((1,), n0, dtype=torch.int32, device="cuda")
     n_b = torch.full((1,), n0, dtype=torch.int32, device="cuda")
     for n in range(n0 + 1, n0 + steps + 1):
