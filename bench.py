@@ -21,7 +21,11 @@ Bytes per step follow the reference's accounting (src/ssa/attn/accounting.py:19-
 (sequence, KV head): selected K+V rows 2*rows*d*2, label scan 2n, 6 B per row read, summaries
 C*(d+12) and centroids C*d (8-bit), inserted key 2d and its cluster's fp32 sum 8d. The step is
 one kernel, so the roofline entry is that kernel: these bytes over its graph-timed duration per
-launch (the mean over replays of the timed region).
+launch (the mean over replays of the timed region). Each budget's detail also times the parts
+the reference reports apart (maint_select and attention in its harness): the fused kernel
+without the insertion (select_attention_us), the selection alone (ssa_select: score and pick
+into w; select_us) and the attention alone given labels and w (ssa_label_attention: label
+scan, split-K attention, merge; labelled_attention_us).
 
 The CPU baseline times the oracle's numpy restatement of the reference's CPU path
 (SphereIndexRef: observe one key, labels_and_weights, label_weighted_attention) at the same
@@ -298,6 +302,9 @@ def main() -> int:
             st.idx.budget = b
         graphs[("step", b)] = capture([lambda st=st: st.idx.step(st.q, st.K, st.V, st.n_dev) for st in sets])
         graphs[("attn", b)] = capture([lambda st=st: _fused_only(st) for st in sets])
+        # the unfused parts, as the reference's maint_select and attention report them
+        graphs[("select", b)] = capture([lambda st=st: _select_only(st) for st in sets])
+        graphs[("lattn", b)] = capture([lambda st=st: _label_attention_only(st) for st in sets])
     for st in sets:
         st.idx.budget = HEADLINE
 
@@ -307,6 +314,8 @@ def main() -> int:
         time_graph(graphs[("step", b)], args.warmup, R, advance=advance)
         res[("step", b)] = time_graph(graphs[("step", b)], reps, R, advance=advance)
         res[("attn", b)] = time_graph(graphs[("attn", b)], reps, R)
+        res[("select", b)] = time_graph(graphs[("select", b)], reps, R)
+        res[("lattn", b)] = time_graph(graphs[("lattn", b)], reps, R)
         res[("rows", b)] = sets[-1].idx.work.cnt.tolist()      # rows read per head, counted by the kernel
     time_graph(graphs["dense"], 3, R)
     res["dense"] = time_graph(graphs["dense"], reps, R)
@@ -342,6 +351,7 @@ def main() -> int:
         step_us, attn_us = res[("step", b)][0], res[("attn", b)][0]
         detail[f"{int(b * 100)}%"] = {
             "step_us": round(step_us, 2), "select_attention_us": round(attn_us, 2),
+            "select_us": round(res[("select", b)][0], 2), "labelled_attention_us": round(res[("lattn", b)][0], 2),
             "rows_per_head": int(sum(rows) / len(rows)),
             "step_effective_GBs": round(step_bytes(rows, N) / step_us / 1e3, 1),
             "attention_GBs": round(attn_bytes(rows, N) / attn_us / 1e3, 1),
@@ -689,6 +699,25 @@ def _profiled_traffic():
     except OSError:
         pass
     return None
+
+
+def _select_only(st):
+    """The selection alone (score + pick into w, ssa_select without insertion): the reference's
+    maint_select part."""
+    from ssa_amd._lib import check, lib, stream_ptr
+    idx = st.idx
+    sel = idx._select_args(st.q, idx.wbuf, idx.budget, "sum_share")
+    check(lib().ssa_select(idx._state(), None, sel, stream_ptr(st.q.device)), "ssa_select")
+
+
+def _label_attention_only(st):
+    """The attention alone, given labels and w (compaction, split-K attention over the selected
+    rows, merge; ssa_label_attention): the reference's attention part."""
+    from ssa_amd._lib import check, lib, stream_ptr
+    from ssa_amd.labeled_attn import attn_args
+    idx = st.idx
+    a = attn_args(st.q, st.K, st.V, idx.out, idx.work, labels=idx.labels, w=idx.wbuf, n_dev=st.n_dev)
+    check(lib().ssa_label_attention(a, stream_ptr(st.q.device)), "ssa_label_attention")
 
 
 def _fused_only(st):
