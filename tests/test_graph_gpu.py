@@ -48,9 +48,10 @@ def _same_state(a, b):
         assert torch.equal(x, y), f
 
 
-# (KV heads, splits): 3 heads stage in an extra workgroup per head; 128 x 4 and 67 x 8 give more
-# than two workgroups per compute unit with one, so split S - 1 of each head stages instead
-@pytest.mark.parametrize("H_kv,splits,steps", [(3, None, 120), (128, 4, 40), (67, 8, 40)])
+# (KV heads, splits): 3 heads stage in an extra workgroup per head; 128 x 4, 67 x 8 and 520 x 1
+# give more than two workgroups per compute unit with one, so split S - 1 of each head stages
+# instead (at S = 1 the head's only workgroup attends, stages, merges and commits)
+@pytest.mark.parametrize("H_kv,splits,steps", [(3, None, 120), (128, 4, 40), (67, 8, 40), (520, 1, 12)])
 @pytest.mark.parametrize("budget", [0.05, 0.2])
 def test_insert_ahead_matches_insertion_at_step_start(budget, H_kv, splits, steps):
     from ssa_amd._lib import check, lib, stream_ptr
