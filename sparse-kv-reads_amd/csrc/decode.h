@@ -562,7 +562,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     cpart = wave_sum_i(cpart);
     if (lane == 0) sm.red_i[0] = cpart;
   }
+  if constexpr (AHEAD) stage_publish(stp, sm.stage_hdr);
   __syncthreads();
+  // Every workgroup of this head has read the index state and the labels (each counted itself in
+  // after its scan, the stager after its stores), so the state may now move to the next step:
+  // commit the staged insertion of the keys that leave the window at length n + 1, as ssa_insert
+  // would bin them at the start of the next step. The one-key stage is a few stores that use no
+  // LDS, issued here so that they overlap the merge; a split or a general stage runs after it.
+  bool committed = false;
+  if constexpr (AHEAD) {
+    if (sm.stage_hdr[0] == kStageOne) {
+      insert_commit<D>(sm.u.tail, a.st, a.ins, h, n + 1, stp, sm.stage_hdr);
+      committed = true;
+    }
+  }
   // rescaled sum of the accumulators: float4 columns, splits strided over thread groups
   for (int c0 = 0; c0 < cols4; c0 += kThreads) {
     const int ncol = min(kThreads, cols4 - c0);
@@ -613,13 +626,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     __hip_atomic_store(a.counter + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if constexpr (AHEAD) {
-    // Every workgroup of this head has read the index state and the labels (each counted itself
-    // in after its scan, the stager after its stores), so the state may now move to the next
-    // step: commit the staged insertion of the keys that leave the window at length n + 1, as
-    // ssa_insert would bin them at the start of the next step.
-    stage_publish(stp, sm.stage_hdr);
-    __syncthreads();                                     // the merge is done with sm.u
-    insert_commit<D>(sm.u.tail, a.st, a.ins, h, n + 1, stp, sm.stage_hdr);
+    if (!committed) {
+      __syncthreads();                                   // the merge is done with sm.u
+      insert_commit<D>(sm.u.tail, a.st, a.ins, h, n + 1, stp, sm.stage_hdr);
+    }
   }
 }
 

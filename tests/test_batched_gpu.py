@@ -97,28 +97,35 @@ def test_config2_8x8k_full_size_step(budget):
     _same(idx, canon)
 
 
+@pytest.mark.parametrize("ahead", [False, True])
 @pytest.mark.parametrize("B,n", [(16, 2048), (64, 1024)])
 @pytest.mark.parametrize("budget", [0.2, 0.05])
-def test_many_heads_steps_match_the_oracle(B, n, budget):
-    """128 and 512 folded heads: the separate insertion launch, the doubled split count and the
-    XCD placement over large grids, for 12 steps, against the full oracle (fit included)."""
+def test_many_heads_steps_match_the_oracle(B, n, budget, ahead):
+    """128 and 512 folded heads: the doubled split count and the XCD placement over large grids,
+    with a separate insertion launch and with insert-ahead (staged by each head's last split: an
+    extra workgroup per head would not be resident), for 12 steps, against the full oracle (fit
+    included)."""
     from ssa_amd.graph_kernels import SphereIndexGraph
     from ssa_amd.sphere_fused import kmeans_init_indices
     C, W, steps = 64, 64, 12
     K, V, q = _folded(B, n, steps + 8, seed=41 + B, centers=C)
     hk = B * H_KV
     idx = SphereIndexGraph(budget=budget, C=C, window=W, delta=0.03, capacity=n + steps + 8, check_every=10 ** 9,
-                           partition="kmeans")
+                           partition="kmeans", insert_ahead=ahead)
     idx.prepare(K, n, B * H)
     from ssa_amd.labeled_attn import cu_count
     cus = cu_count(q.device)
-    assert not idx.insert_ahead                               # 4 x heads > compute units: separate insertion
+    assert idx.insert_ahead == ahead
     assert -(-cus // hk) <= 2 and idx.work.S == max(1, -(-2 * cus // hk))   # two workgroups per compute unit
+    if ahead:
+        assert hk * (idx.work.S + 1) > 2 * cus                # the stage folds into split S - 1
     Kf = K.float().cpu().numpy()                              # the oracle's fp32 copy of the cache
     canon = CanonIndex(hk, D, C=C, capacity=idx.capacity, C_init=C, partition="kmeans", summary_bits=8, ms=idx.MS)
     end0 = n - W
     canon.build(Kf, start=1, end=end0, fit=True, iters=idx.kmeans_iters,
                 init_idx=kmeans_init_indices(end0 - 1, C, idx.seed).numpy())
+    if ahead:                                                 # prepare binned the first step's keys
+        canon.insert(Kf, n + 1, window=W, delta=0.03)
     _same(idx, canon)
     n_dev = torch.full((1,), n, dtype=torch.int32, device="cuda")
     for m in range(n + 1, n + steps + 1):
@@ -131,6 +138,8 @@ def test_many_heads_steps_match_the_oracle(B, n, budget):
         assert idx.work.cnt.tolist() == [len(p) for p in canon.compact(want_w, m)], m
         if m == n + steps:
             _check_output(out, q, K, V, canon.labels, want_w, m)
+    if ahead:                                                 # the last step binned the next length's keys
+        canon.insert(Kf, n + steps + 1, window=W, delta=0.03)
     _same(idx, canon)
 
 
