@@ -295,12 +295,49 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)h * a.s_vh + li * 8;
     int rows_read = 0;
 
-    // pages: dense, kPage consecutive positions of [s0, s1); label scans, PER interleaved blocks
-    for (int it = 0, p0 = s0; DENSE ? p0 < s1 : block_pos(it, 0) < n; ++it, p0 += kPage) {
+    // Fused mode: the positions [ex0, n) not yet binned (label C, the exact set) are always read.
+    // They are left out of the label scans and dealt round robin over the splits, so that the
+    // recent window does not all fall to the split owning the last block (at 20% that split read
+    // 64 rows above the ~210 of every other one, a third batch of row loads that the merge waited
+    // for). Compiled up to two query heads per KV head: past that the kernel has no registers to
+    // spare for it (it would drop to one wave per SIMD).
+    constexpr bool SPREAD = SELECT && GMAX <= 2;
+    const int ex0 = SPREAD ? min(max(end_h, 1), n) : n;
+    const int nblk = (ex0 + kThreads - 1) / kThreads;          // blocks the label scans cover
+    const int nscan = DENSE ? 0 : max(0, (nblk - sp + S * PER - 1) / (S * PER));
+    // pages: dense, kPage consecutive positions of [s0, s1); label scans, PER interleaved blocks,
+    // with this split's share of the exact set (positions ex0 + sp + S i) appended to the last
+    // scanned page's list, or in pages of its own when it does not fit there
+    bool xin = false;
+    for (int it = 0, p0 = s0;; ++it, p0 += kPage) {
+      if constexpr (DENSE) {
+        if (p0 >= s1) break;
+      } else {
+        if (it >= nscan && (!SPREAD || xin || ex0 + S * kPage * (it - nscan) + sp >= n)) break;
+      }
       const int pn = min(kPage, s1 - p0);
       int R;
       if constexpr (DENSE) {
         R = pn;
+      } else if (SPREAD && it >= nscan) {
+        __syncthreads();   // previous page's list consumed
+        const int base = ex0 + S * kPage * (it - nscan) + sp;
+        const int cx = a.w_len - 1;                            // the exact set's slot
+#pragma unroll 1
+        for (int u = 0; u < PER; ++u) {
+          const int i = tid + kThreads * u;
+          const int p = base + S * i;
+          if (p < n) {
+            sm.u.list.pos[i] = p;
+            if (per_head) {
+              for (int g = 0; g < G; ++g) sm.u.list.rlw[g][i] = sm.lw[g][cx];
+            } else {
+              sm.u.list.rlw[0][i] = sm.lw[0][cx];
+            }
+          }
+        }
+        R = min(kPage, (n - base + S - 1) / S);
+        __syncthreads();
       } else {
         // lbl holds this page's labels: the first page's were loaded at the start, each later
         // page's while the previous page's rows were read
@@ -312,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
           const int j = block_pos(it, u) + tid;
           lbl[u] = min(max(lbl[u], 0), a.w_len - 1);     // a bad label never indexes outside lw
           bool s = false;
-          if (j < n) {
+          if (j < ex0) {
             if (per_head) {
               for (int g = 0; g < G; ++g) s |= sm.lw[g][lbl[u]] != -INFINITY;
             } else {
@@ -351,6 +388,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
           total += tot_u;
         }
         R = total;
+        if constexpr (SPREAD) {
+          const int nx = n > ex0 + sp ? (n - ex0 - sp + S - 1) / S : 0;
+          if (it == nscan - 1 && total + nx <= kPage) {
+            const int cx = a.w_len - 1;                        // the exact set's slot
+            for (int i = tid; i < nx; i += kThreads) {
+              sm.u.list.pos[total + i] = ex0 + sp + S * i;
+              if (per_head) {
+                for (int g = 0; g < G; ++g) sm.u.list.rlw[g][total + i] = sm.lw[g][cx];
+              } else {
+                sm.u.list.rlw[0][total + i] = sm.lw[0][cx];
+              }
+            }
+            R = total + nx;
+            xin = true;
+          }
+        }
         // the next page's labels load while this page's rows are read
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
