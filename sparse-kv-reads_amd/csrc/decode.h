@@ -296,48 +296,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
     int rows_read = 0;
 
     // Fused mode: the positions [ex0, n) not yet binned (label C, the exact set) are always read.
-    // They are left out of the label scans and dealt round robin over the splits, so that the
-    // recent window does not all fall to the split owning the last block (at 20% that split read
-    // 64 rows above the ~210 of every other one, a third batch of row loads that the merge waited
-    // for). Compiled up to two query heads per KV head: past that the kernel has no registers to
-    // spare for it (it would drop to one wave per SIMD).
+    // They are left out of the label scans and dealt round robin over the splits, appended to
+    // each split's last scanned page, so that the recent window does not all fall to the split
+    // owning the last block (at 20% that split read 64 rows above the ~210 of every other one, a
+    // third batch of row loads that the merge waited for). Taken when it fits every split's last
+    // page (every split has a block and no last page is full: the head's splits all decide
+    // alike, from n, end and S); otherwise the exact set stays in the scans. Compiled up to two
+    // query heads per KV head: past that the kernel has no registers to spare for it (it would
+    // drop to one wave per SIMD).
     constexpr bool SPREAD = SELECT && GMAX <= 2;
-    const int ex0 = SPREAD ? min(max(end_h, 1), n) : n;
+    int ex0 = n;
+    if constexpr (SPREAD) {
+      const int e0 = min(max(end_h, 1), n);
+      const int nb = (e0 + kThreads - 1) / kThreads, q = nb / S, r = nb % S;
+      if (n - e0 <= kThreads * S && q >= 1 && q % PER != 0 && (r == 0 || (q + 1) % PER != 0)) ex0 = e0;
+    }
     const int nblk = (ex0 + kThreads - 1) / kThreads;          // blocks the label scans cover
     const int nscan = DENSE ? 0 : max(0, (nblk - sp + S * PER - 1) / (S * PER));
-    // pages: dense, kPage consecutive positions of [s0, s1); label scans, PER interleaved blocks,
-    // with this split's share of the exact set (positions ex0 + sp + S i) appended to the last
-    // scanned page's list, or in pages of its own when it does not fit there
-    bool xin = false;
-    for (int it = 0, p0 = s0;; ++it, p0 += kPage) {
-      if constexpr (DENSE) {
-        if (p0 >= s1) break;
-      } else {
-        if (it >= nscan && (!SPREAD || xin || ex0 + S * kPage * (it - nscan) + sp >= n)) break;
-      }
+    // pages: dense, kPage consecutive positions of [s0, s1); label scans, PER interleaved blocks
+    for (int it = 0, p0 = s0; DENSE ? p0 < s1 : it < nscan; ++it, p0 += kPage) {
       const int pn = min(kPage, s1 - p0);
       int R;
       if constexpr (DENSE) {
         R = pn;
-      } else if (SPREAD && it >= nscan) {
-        __syncthreads();   // previous page's list consumed
-        const int base = ex0 + S * kPage * (it - nscan) + sp;
-        const int cx = a.w_len - 1;                            // the exact set's slot
-#pragma unroll 1
-        for (int u = 0; u < PER; ++u) {
-          const int i = tid + kThreads * u;
-          const int p = base + S * i;
-          if (p < n) {
-            sm.u.list.pos[i] = p;
-            if (per_head) {
-              for (int g = 0; g < G; ++g) sm.u.list.rlw[g][i] = sm.lw[g][cx];
-            } else {
-              sm.u.list.rlw[0][i] = sm.lw[0][cx];
-            }
-          }
-        }
-        R = min(kPage, (n - base + S - 1) / S);
-        __syncthreads();
       } else {
         // lbl holds this page's labels: the first page's were loaded at the start, each later
         // page's while the previous page's rows were read
@@ -389,8 +370,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
         }
         R = total;
         if constexpr (SPREAD) {
-          const int nx = n > ex0 + sp ? (n - ex0 - sp + S - 1) / S : 0;
-          if (it == nscan - 1 && total + nx <= kPage) {
+          if (it == nscan - 1 && ex0 < n) {   // room: the last page has at most kPage - kThreads positions
+            const int nx = n > ex0 + sp ? (n - ex0 - sp + S - 1) / S : 0;
             const int cx = a.w_len - 1;                        // the exact set's slot
             for (int i = tid; i < nx; i += kThreads) {
               sm.u.list.pos[total + i] = ex0 + sp + S * i;
@@ -401,7 +382,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams a) {
               }
             }
             R = total + nx;
-            xin = true;
           }
         }
         // the next page's labels load while this page's rows are read
